@@ -1,0 +1,702 @@
+// Block attention over the static / paged block KV cache, gfx950.
+//
+// Semantics: out = softmax(q k^T * scale + M) v per query row, GQA head map
+// h -> h / G (repeat_kv, modeling.py:202-211), with the masks of
+// fdllm_hip.h (seqused: static_kv_cache.py:295-302 and tests/test_focus.py:220-224;
+// block-causal: modeling.py:145-150). This is the operation that
+// AttentionBackend.flash_kvcache_attention (utils/attention_backends.py:588-640)
+// dispatches to flash_attn_with_kvcache.
+//
+// Kernel design (one workgroup = 4 wavefronts = 256 threads):
+//   * Rows. The Sq query tokens x G query heads that share one KV head form the
+//     M dimension: row r = t * G + hh. For the 8-token sub-block decode that is
+//     56 rows (padded to 64); for a 32-token block 224 rows. Each wave owns MT
+//     16-row M-tiles, so a workgroup covers 64 * MT rows and every K/V byte
+//     fetched from HBM serves all G heads of the group.
+//   * Keys. Each workgroup streams one split of the sequence's keys in tiles of
+//     64. A tile is loaded with coalesced 16-byte global loads into registers
+//     one iteration ahead (double buffering through registers), then written
+//     to LDS: K row-major with a 16-byte row pad, V transposed ([d][key]) with
+//     an 8-byte row pad, so that both MFMA operands are read as contiguous
+//     LDS vectors without bank conflicts.
+//   * Math. S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (keys along M, query rows
+//     along N, so each lane owns one query row), online softmax in the base-2
+//     domain with a 4-lane-group max reduction, then O^T = V^T P^T with the
+//     same instruction; P is re-packed to bf16 straight from the S^T
+//     accumulators (the key order inside one 32-key MFMA step is permuted
+//     consistently for P and V, which leaves the sum unchanged).
+//   * Masks are arithmetic: key < row limit, where the limit per row comes from
+//     seqlens / q_start / mask_block. Keys past the limit are never loaded.
+//   * Split-KV. When one (sequence, KV head) is split over several workgroups,
+//     each writes an unnormalised partial (O, m, l) to the workspace, and the
+//     last workgroup to finish (device-scope counter) merges them and writes
+//     the output, then re-arms the counter. No second kernel launch.
+#include <algorithm>
+
+#include "fdllm_common.h"
+
+namespace fdllm {
+namespace {
+
+constexpr int kKT = 64;        // keys per tile
+constexpr int kThreads = 256;  // 4 waves
+
+struct AttnParams {
+  const uint16_t* q;
+  int64_t q_sb, q_ss, q_sh;
+  const uint16_t* k;
+  int64_t k_sp, k_ss, k_sh;
+  const uint16_t* v;
+  int64_t v_sp, v_ss, v_sh;
+  uint16_t* out;
+  int64_t o_sb, o_ss, o_sh;
+  const int32_t* page_table;
+  const int32_t* seqlens;
+  const int32_t* q_start;
+  int max_pages, page_size, max_seqlen;
+  int B, Sq, Hq, Hkv, G;
+  int R;            // rows per (b, kv head) = Sq * G
+  int rows_per_wg;  // 64 * MT
+  int n_rb;         // row blocks per (b, kv head)
+  int n_splits;     // split slots per row block (grid x)
+  int chunk;        // keys per split, multiple of kKT
+  int mask_mode, mask_block;
+  float scale_log2;  // softmax_scale * log2(e)
+  float* ws_o;       // [units, n_splits, rows_per_wg, D]
+  float2* ws_ml;     // [units, n_splits, rows_per_wg]
+  int* ws_cnt;       // [units]
+};
+
+template <bool F16>
+__device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
+  if constexpr (F16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  }
+}
+
+template <bool F16>
+__device__ __forceinline__ uint32_t pack2(float a, float b) {
+  if constexpr (F16) {
+    return Elt<f16_t>::pack(a, b);
+  } else {
+    return Elt<bf16_t>::pack(a, b);
+  }
+}
+
+// Exclusive key bound for query token t of sequence b.
+__device__ __forceinline__ int row_key_limit(const AttnParams& p, int seqlen, int qs, int t) {
+  if (p.mask_mode == FDLLM_MASK_SEQLEN) return seqlen;
+  const int qpos = qs + t;
+  int lim;
+  if (p.mask_mode == FDLLM_MASK_CAUSAL) {
+    lim = qpos + 1;
+  } else {
+    lim = qpos >= 0 ? (qpos / p.mask_block + 1) * p.mask_block : 0;
+  }
+  return lim < seqlen ? lim : seqlen;
+}
+
+// Pointer to row (key j, kv head h) of the K or V pool for sequence b.
+__device__ __forceinline__ int64_t kv_offset(const AttnParams& p, int b, int j, int64_t sp, int64_t ss) {
+  if (p.page_table) {
+    const int page = p.page_table[static_cast<int64_t>(b) * p.max_pages + j / p.page_size];
+    return page * sp + (j % p.page_size) * ss;
+  }
+  return b * sp + j * ss;
+}
+
+template <int D, int MT, bool F16>
+__global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
+  constexpr int KS = D + 8;      // K row stride in LDS (elements), 16-byte pad
+  constexpr int VS = kKT + 4;    // V^T row stride in LDS (elements), 8-byte pad
+  constexpr int NKS = D / 32;    // MFMA k-steps over d for S
+  constexpr int NDT = D / 16;    // 16-wide d tiles of O
+  constexpr int KCH = D / 8;     // 16-byte chunks per key row
+  constexpr int KLD = kKT * KCH / kThreads;  // K 16-byte loads per thread per tile
+  static_assert(KLD >= 1, "tile too small");
+  __shared__ __attribute__((aligned(16))) uint16_t sK[kKT * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t sVt[D * VS];
+  __shared__ int s_is_last;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+
+  const int split = blockIdx.x;
+  const int rb = p.n_rb - 1 - static_cast<int>(blockIdx.y);  // heaviest row blocks first under causal masks
+  const int bh = blockIdx.z;
+  const int b = bh / p.Hkv;
+  const int kvh = bh - b * p.Hkv;
+  const int unit = bh * p.n_rb + rb;
+
+  int seqlen = p.seqlens[b];
+  if (seqlen > p.max_seqlen) seqlen = p.max_seqlen;
+  if (p.page_table && seqlen > p.max_pages * p.page_size) seqlen = p.max_pages * p.page_size;
+  if (seqlen < 0) seqlen = 0;
+  const int qs = p.q_start ? p.q_start[b] : seqlen - p.Sq;
+
+  // Key range of this workgroup: up to the limit of its last valid row.
+  const int row0 = rb * p.rows_per_wg;
+  const int row_last = min(p.R, row0 + p.rows_per_wg) - 1;
+  const int kv_end = max(0, row_key_limit(p, seqlen, qs, row_last / p.G));
+  const int n_act = (kv_end + p.chunk - 1) / p.chunk;
+  if (split >= max(n_act, 1)) return;
+  const int k_lo = split * p.chunk;
+  const int k_hi = min(kv_end, k_lo + p.chunk);
+
+  // ---- per-lane query rows, Q fragments (B operand of S^T = K Q^T), row limits
+  u32x4 qf[MT][NKS];
+  int lim[MT];
+  bool mt_valid[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int r = row0 + (wave * MT + mt) * 16 + l16;
+    mt_valid[mt] = (row0 + (wave * MT + mt) * 16) < p.R;
+    if (r < p.R) {
+      const int t = r / p.G;
+      const int hh = r - t * p.G;
+      lim[mt] = row_key_limit(p, seqlen, qs, t);
+      const uint16_t* qrow = p.q + b * p.q_sb + t * p.q_ss + (kvh * p.G + hh) * p.q_sh;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) qf[mt][ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 32 + g * 8);
+    } else {
+      lim[mt] = 0;
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks) qf[mt][ks] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  f32x4 acc[MT][NDT];
+  float m_run[MT], l_run[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    m_run[mt] = -INFINITY;
+    l_run[mt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[mt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // ---- global -> register staging of one 64-key tile
+  u32x4 kreg[KLD];
+  u32x4 vreg[4];
+  const int v_kq = tid & 15;   // key quad
+  const int v_dq = tid >> 4;   // d octet
+  const bool v_active = v_dq < KCH;
+  auto load_tile = [&](int kb) {
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int c = tid + kThreads * i;
+      const int key = kb + c / KCH;
+      const int dc = c % KCH;
+      if (key < k_hi) {
+        kreg[i] = *reinterpret_cast<const u32x4*>(p.k + kv_offset(p, b, key, p.k_sp, p.k_ss) + kvh * p.k_sh + dc * 8);
+      } else {
+        kreg[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    if (v_active) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int key = kb + v_kq * 4 + r;
+        if (key < k_hi) {
+          vreg[r] =
+              *reinterpret_cast<const u32x4*>(p.v + kv_offset(p, b, key, p.v_sp, p.v_ss) + kvh * p.v_sh + v_dq * 8);
+        } else {
+          vreg[r] = u32x4{0u, 0u, 0u, 0u};
+        }
+      }
+    }
+  };
+  auto store_tile = [&]() {
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int c = tid + kThreads * i;
+      *reinterpret_cast<u32x4*>(&sK[(c / KCH) * KS + (c % KCH) * 8]) = kreg[i];
+    }
+    if (v_active) {
+      // 4 keys x 8 d  ->  8 rows of V^T, 4 consecutive keys each (8 bytes)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int w = e >> 1;
+        uint32_t lo, hi;
+        if (e & 1) {
+          lo = (vreg[0][w] >> 16) | (vreg[1][w] & 0xffff0000u);
+          hi = (vreg[2][w] >> 16) | (vreg[3][w] & 0xffff0000u);
+        } else {
+          lo = (vreg[0][w] & 0xffffu) | (vreg[1][w] << 16);
+          hi = (vreg[2][w] & 0xffffu) | (vreg[3][w] << 16);
+        }
+        *reinterpret_cast<u32x2*>(&sVt[(v_dq * 8 + e) * VS + v_kq * 4]) = u32x2{lo, hi};
+      }
+    }
+  };
+
+  if (k_lo < k_hi) load_tile(k_lo);
+  for (int kb = k_lo; kb < k_hi; kb += kKT) {
+    __syncthreads();  // previous tile fully consumed
+    store_tile();
+    __syncthreads();
+    if (kb + kKT < k_hi) load_tile(kb + kKT);
+
+    // ---- S^T = K Q^T for four 16-key sub-tiles
+    f32x4 s[MT][4];
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      u32x4 kf[NKS];
+#pragma unroll
+      for (int ks = 0; ks < NKS; ++ks)
+        kf[ks] = *reinterpret_cast<const u32x4*>(&sK[(st * 16 + l16) * KS + ks * 32 + g * 8]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+        if (mt_valid[mt]) {
+#pragma unroll
+          for (int ks = 0; ks < NKS; ++ks) c = mfma16x16x32<F16>(kf[ks], qf[mt][ks], c);
+        }
+        s[mt][st] = c;
+      }
+    }
+
+    // ---- online softmax (base 2); lane owns query row l16 of each M-tile
+    u32x4 pf[MT][2];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int key = kb + st * 16 + g * 4 + j;
+          const float x = key < lim[mt] ? s[mt][st][j] * p.scale_log2 : -INFINITY;
+          s[mt][st][j] = x;
+          tmax = fmaxf(tmax, x);
+        }
+      }
+      tmax = group4_allreduce_max(tmax);
+      const float m_new = fmaxf(m_run[mt], tmax);
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float alpha = exp2f(m_run[mt] - m_use);
+      m_run[mt] = m_new;
+      float lsum = 0.f;
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = exp2f(s[mt][st][j] - m_use);
+          s[mt][st][j] = e;
+          lsum += e;
+        }
+      }
+      l_run[mt] = l_run[mt] * alpha + lsum;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) acc[mt][dt] *= alpha;
+      // B operand of O^T = V^T P^T for key steps kk = 0, 1:
+      // k-index 8g + j <-> key 32kk + 4g + j (j < 4), 32kk + 16 + 4g + (j - 4) (j >= 4)
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        pf[mt][kk][0] = pack2<F16>(s[mt][2 * kk][0], s[mt][2 * kk][1]);
+        pf[mt][kk][1] = pack2<F16>(s[mt][2 * kk][2], s[mt][2 * kk][3]);
+        pf[mt][kk][2] = pack2<F16>(s[mt][2 * kk + 1][0], s[mt][2 * kk + 1][1]);
+        pf[mt][kk][3] = pack2<F16>(s[mt][2 * kk + 1][2], s[mt][2 * kk + 1][3]);
+      }
+    }
+
+    // ---- O^T += V^T P^T
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const uint16_t* vrow = &sVt[(dt * 16 + l16) * VS + kk * 32 + g * 4];
+        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
+        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
+        const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          if (mt_valid[mt]) acc[mt][dt] = mfma16x16x32<F16>(vf, pf[mt][kk], acc[mt][dt]);
+        }
+      }
+    }
+  }
+
+  // ---- epilogue
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) l_run[mt] = group4_allreduce_sum(l_run[mt]);
+
+  if (n_act <= 1) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int r = row0 + (wave * MT + mt) * 16 + l16;
+      if (r >= p.R) continue;
+      const int t = r / p.G;
+      const int hh = r - t * p.G;
+      const float inv = l_run[mt] > 0.f ? 1.f / l_run[mt] : 0.f;
+      uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const f32x4 o = acc[mt][dt] * inv;
+        *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) = u32x2{pack2<F16>(o[0], o[1]), pack2<F16>(o[2], o[3])};
+      }
+    }
+    return;
+  }
+
+  // split: publish this workgroup's partial
+  const int64_t slot = static_cast<int64_t>(unit) * p.n_splits + split;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int rl = (wave * MT + mt) * 16 + l16;
+    float* po = p.ws_o + (slot * p.rows_per_wg + rl) * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16 + g * 4) = acc[mt][dt];
+    if (g == 0) p.ws_ml[slot * p.rows_per_wg + rl] = make_float2(m_run[mt], l_run[mt]);
+  }
+  __threadfence();
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = atomicAdd(&p.ws_cnt[unit], 1);
+    s_is_last = (prev == n_act - 1);
+  }
+  __syncthreads();
+  if (!s_is_last) return;
+  __threadfence();
+
+  // last workgroup: merge n_act partials per row, 4 threads per row, D/4 columns each
+  constexpr int DQ = D / 4;
+  for (int rl = tid >> 2; rl < p.rows_per_wg; rl += kThreads / 4) {
+    const int r = row0 + rl;
+    if (r >= p.R) continue;
+    const int d0 = (tid & 3) * DQ;
+    float mmax = -INFINITY;
+    for (int sp = 0; sp < n_act; ++sp) {
+      const float2 ml = p.ws_ml[(static_cast<int64_t>(unit) * p.n_splits + sp) * p.rows_per_wg + rl];
+      mmax = fmaxf(mmax, ml.x);
+    }
+    const float m_use = mmax == -INFINITY ? 0.f : mmax;
+    float o[DQ];
+#pragma unroll
+    for (int i = 0; i < DQ; ++i) o[i] = 0.f;
+    float lsum = 0.f;
+    for (int sp = 0; sp < n_act; ++sp) {
+      const int64_t sl = (static_cast<int64_t>(unit) * p.n_splits + sp) * p.rows_per_wg + rl;
+      const float2 ml = p.ws_ml[sl];
+      const float w = exp2f(ml.x - m_use);
+      lsum += w * ml.y;
+      const f32x4* po = reinterpret_cast<const f32x4*>(p.ws_o + sl * D + d0);
+#pragma unroll
+      for (int i = 0; i < DQ / 4; ++i) {
+        const f32x4 x = po[i];
+        o[4 * i + 0] += w * x[0];
+        o[4 * i + 1] += w * x[1];
+        o[4 * i + 2] += w * x[2];
+        o[4 * i + 3] += w * x[3];
+      }
+    }
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+    const int t = r / p.G;
+    const int hh = r - t * p.G;
+    uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh + d0;
+#pragma unroll
+    for (int i = 0; i < DQ / 8; ++i) {
+      u32x4 w4;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) w4[j] = pack2<F16>(o[8 * i + 2 * j] * inv, o[8 * i + 2 * j + 1] * inv);
+      *reinterpret_cast<u32x4*>(orow + 8 * i) = w4;
+    }
+  }
+  if (tid == 0) atomicExch(&p.ws_cnt[unit], 0);  // re-arm for the next call
+}
+
+// ---------------------------------------------------------------------------
+// KV cache write (StaticKVCache.update / write_scratch_compiled / write_sparse)
+// ---------------------------------------------------------------------------
+struct KVWriteArgs {
+  const uint16_t* k_new;
+  const uint16_t* v_new;
+  int64_t n_sb, n_ss, n_sh;
+  uint16_t* k_cache;
+  uint16_t* v_cache;
+  int64_t c_sp, c_ss, c_sh;
+  const int32_t* page_table;
+  int max_pages, page_size, max_seqlen;
+  const int32_t* write_start;
+  int write_offset;
+  const int64_t* positions;
+  int B, T, Hkv, D;
+};
+
+// One 16-byte vector per thread; grid covers B * T * Hkv * D / 8 vectors.
+__global__ __launch_bounds__(256) void kv_write_kernel(const KVWriteArgs a) {
+  const int dch = a.D / 8;
+  const int64_t n = static_cast<int64_t>(a.B) * a.T * a.Hkv * dch;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int dc = static_cast<int>(i % dch);
+  int64_t rest = i / dch;
+  const int h = static_cast<int>(rest % a.Hkv);
+  rest /= a.Hkv;
+  const int t = static_cast<int>(rest % a.T);
+  const int b = static_cast<int>(rest / a.T);
+  int64_t pos;
+  if (a.positions) {
+    pos = a.positions[static_cast<int64_t>(b) * a.T + t];
+  } else {
+    pos = static_cast<int64_t>(a.write_start ? a.write_start[b] : a.write_offset) + t;
+  }
+  int64_t off;
+  if (a.page_table) {
+    if (pos < 0 || pos >= static_cast<int64_t>(a.max_pages) * a.page_size) return;
+    const int page = a.page_table[static_cast<int64_t>(b) * a.max_pages + pos / a.page_size];
+    off = page * a.c_sp + (pos % a.page_size) * a.c_ss;
+  } else {
+    if (pos < 0 || pos >= a.max_seqlen) return;
+    off = b * a.c_sp + pos * a.c_ss;
+  }
+  off += h * a.c_sh + dc * 8;
+  const int64_t src = b * a.n_sb + t * a.n_ss + h * a.n_sh + dc * 8;
+  *reinterpret_cast<u32x4*>(a.k_cache + off) = *reinterpret_cast<const u32x4*>(a.k_new + src);
+  *reinterpret_cast<u32x4*>(a.v_cache + off) = *reinterpret_cast<const u32x4*>(a.v_new + src);
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Workspace layout: a fixed header of completion counters, then the split-KV
+// partials. The header never holds partial data, so once zero-filled it stays
+// zero between calls (every completed call re-arms the counters it used), no
+// matter how the sizes of consecutive calls differ.
+constexpr size_t kCounterBytes = 16384;
+constexpr int64_t kMaxSplitUnits = kCounterBytes / sizeof(int);
+
+struct Plan {
+  int MT, rows_per_wg, n_rb, n_splits, chunk, R;
+  size_t ws_o_bytes, ws_ml_bytes, ws_cnt_bytes;
+};
+
+int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
+  FDLLM_CHECK_ARG(d != nullptr, "fdllm_kv_attn: null descriptor");
+  FDLLM_CHECK_ARG(d->dtype == FDLLM_DTYPE_BF16 || d->dtype == FDLLM_DTYPE_F16,
+                  "fdllm_kv_attn: dtype %d unsupported (bf16 or fp16 only)", d->dtype);
+  FDLLM_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128, "fdllm_kv_attn: head_dim %d unsupported (64 or 128)",
+                  d->head_dim);
+  FDLLM_CHECK_ARG(d->batch >= 0 && d->q_len >= 0 && d->num_q_heads > 0 && d->num_kv_heads > 0,
+                  "fdllm_kv_attn: bad sizes");
+  FDLLM_CHECK_ARG(d->num_q_heads % d->num_kv_heads == 0, "fdllm_kv_attn: num_q_heads %d not a multiple of %d",
+                  d->num_q_heads, d->num_kv_heads);
+  FDLLM_CHECK_ARG(d->max_seqlen >= 0, "fdllm_kv_attn: max_seqlen < 0");
+  FDLLM_CHECK_ARG(d->mask_mode >= FDLLM_MASK_SEQLEN && d->mask_mode <= FDLLM_MASK_BLOCK_CAUSAL,
+                  "fdllm_kv_attn: unknown mask_mode %d", d->mask_mode);
+  FDLLM_CHECK_ARG(d->mask_mode != FDLLM_MASK_BLOCK_CAUSAL || d->mask_block > 0,
+                  "fdllm_kv_attn: block-causal mask needs mask_block > 0");
+  FDLLM_CHECK_ARG(d->page_table == nullptr || (d->page_size > 0 && d->max_pages > 0),
+                  "fdllm_kv_attn: page table needs page_size > 0 and max_pages > 0");
+  FDLLM_CHECK_ARG(d->kv_split >= 0 && d->kv_split % kKT == 0, "fdllm_kv_attn: kv_split %d not a multiple of %d",
+                  d->kv_split, kKT);
+  const int G = d->num_q_heads / d->num_kv_heads;
+  const int64_t R64 = static_cast<int64_t>(d->q_len) * G;
+  FDLLM_CHECK_ARG(R64 < (1 << 30), "fdllm_kv_attn: q_len * group too large");
+  pl->R = static_cast<int>(R64);
+  const int mtiles = (pl->R + 15) / 16;
+  pl->MT = mtiles <= 4 ? 1 : (mtiles <= 8 ? 2 : 4);
+  pl->rows_per_wg = 64 * pl->MT;
+  pl->n_rb = (pl->R + pl->rows_per_wg - 1) / pl->rows_per_wg;
+  const int max_len = d->page_table ? std::min<int64_t>(d->max_seqlen, static_cast<int64_t>(d->max_pages) * d->page_size)
+                                    : d->max_seqlen;
+  const int max_tiles = std::max(1, (max_len + kKT - 1) / kKT);
+  int chunk_tiles;
+  if (d->kv_split > 0) {
+    chunk_tiles = d->kv_split / kKT;
+  } else {
+    // Aim for ~2 workgroups per CU (256 CUs) when every sequence is full length.
+    const int64_t units = static_cast<int64_t>(d->batch) * d->num_kv_heads * pl->n_rb;
+    const int64_t target = 512;
+    if (units >= target) {
+      chunk_tiles = max_tiles;
+    } else {
+      const int64_t splits = (target + units - 1) / std::max<int64_t>(units, 1);
+      chunk_tiles = static_cast<int>((max_tiles + splits - 1) / splits);
+      chunk_tiles = std::max(chunk_tiles, 4);  // >= 256 keys per split keeps partial traffic small
+    }
+  }
+  chunk_tiles = std::max(1, std::min(chunk_tiles, max_tiles));
+  const int64_t units = static_cast<int64_t>(d->batch) * d->num_kv_heads * pl->n_rb;
+  if (units > kMaxSplitUnits) chunk_tiles = max_tiles;  // enough parallelism; no counters to spare
+  pl->chunk = chunk_tiles * kKT;
+  pl->n_splits = (max_tiles + chunk_tiles - 1) / chunk_tiles;
+  if (pl->n_splits > 1) {
+    pl->ws_o_bytes = static_cast<size_t>(units) * pl->n_splits * pl->rows_per_wg * d->head_dim * sizeof(float);
+    pl->ws_ml_bytes = static_cast<size_t>(units) * pl->n_splits * pl->rows_per_wg * sizeof(float2);
+    pl->ws_cnt_bytes = kCounterBytes;
+  } else {
+    pl->ws_o_bytes = pl->ws_ml_bytes = pl->ws_cnt_bytes = 0;
+  }
+  return FDLLM_OK;
+}
+
+inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+template <int D, int MT>
+void launch_attn(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
+  if (f16) {
+    kv_attn_kernel<D, MT, true><<<grid, dim3(kThreads), 0, s>>>(p);
+  } else {
+    kv_attn_kernel<D, MT, false><<<grid, dim3(kThreads), 0, s>>>(p);
+  }
+}
+
+}  // namespace
+}  // namespace fdllm
+
+extern "C" int fdllm_kv_attn_workspace_size(const fdllm_kv_attn_desc* desc, size_t* bytes) {
+  using namespace fdllm;
+  FDLLM_CHECK_ARG(bytes != nullptr, "fdllm_kv_attn_workspace_size: null output");
+  Plan pl;
+  const int rc = make_plan(desc, &pl);
+  if (rc != FDLLM_OK) return rc;
+  *bytes = pl.n_splits > 1 ? align256(pl.ws_cnt_bytes) + align256(pl.ws_ml_bytes) + pl.ws_o_bytes : 0;
+  return FDLLM_OK;
+}
+
+extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  using namespace fdllm;
+  Plan pl;
+  const int rc = make_plan(d, &pl);
+  if (rc != FDLLM_OK) return rc;
+  if (d->batch == 0 || d->q_len == 0) return FDLLM_OK;
+  FDLLM_CHECK_ARG(d->q && d->k && d->v && d->out && d->seqlens, "fdllm_kv_attn_fwd: null pointer");
+  FDLLM_CHECK_ARG(aligned16(d->q) && aligned16(d->k) && aligned16(d->v) && aligned16(d->out),
+                  "fdllm_kv_attn_fwd: q/k/v/out must be 16-byte aligned");
+  FDLLM_CHECK_ARG(d->q_stride_b % 8 == 0 && d->q_stride_s % 8 == 0 && d->q_stride_h % 8 == 0 &&
+                      d->k_stride_page % 8 == 0 && d->k_stride_slot % 8 == 0 && d->k_stride_h % 8 == 0 &&
+                      d->v_stride_page % 8 == 0 && d->v_stride_slot % 8 == 0 && d->v_stride_h % 8 == 0 &&
+                      d->out_stride_b % 8 == 0 && d->out_stride_s % 8 == 0 && d->out_stride_h % 8 == 0,
+                  "fdllm_kv_attn_fwd: strides must be multiples of 8 elements");
+  const size_t need = pl.n_splits > 1 ? align256(pl.ws_cnt_bytes) + align256(pl.ws_ml_bytes) + pl.ws_o_bytes : 0;
+  if (need > 0) {
+    if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)) {
+      set_last_error("fdllm_kv_attn_fwd: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
+      return FDLLM_ERR_WORKSPACE;
+    }
+  }
+  const int64_t grid_z = static_cast<int64_t>(d->batch) * d->num_kv_heads;
+  FDLLM_CHECK_ARG(grid_z < 65536 && pl.n_rb < 65536, "fdllm_kv_attn_fwd: grid too large");
+
+  AttnParams p;
+  p.q = static_cast<const uint16_t*>(d->q);
+  p.q_sb = d->q_stride_b;
+  p.q_ss = d->q_stride_s;
+  p.q_sh = d->q_stride_h;
+  p.k = static_cast<const uint16_t*>(d->k);
+  p.k_sp = d->k_stride_page;
+  p.k_ss = d->k_stride_slot;
+  p.k_sh = d->k_stride_h;
+  p.v = static_cast<const uint16_t*>(d->v);
+  p.v_sp = d->v_stride_page;
+  p.v_ss = d->v_stride_slot;
+  p.v_sh = d->v_stride_h;
+  p.out = static_cast<uint16_t*>(d->out);
+  p.o_sb = d->out_stride_b;
+  p.o_ss = d->out_stride_s;
+  p.o_sh = d->out_stride_h;
+  p.page_table = d->page_table;
+  p.seqlens = d->seqlens;
+  p.q_start = d->q_start;
+  p.max_pages = d->max_pages;
+  p.page_size = d->page_size;
+  p.max_seqlen = d->max_seqlen;
+  p.B = d->batch;
+  p.Sq = d->q_len;
+  p.Hq = d->num_q_heads;
+  p.Hkv = d->num_kv_heads;
+  p.G = d->num_q_heads / d->num_kv_heads;
+  p.R = pl.R;
+  p.rows_per_wg = pl.rows_per_wg;
+  p.n_rb = pl.n_rb;
+  p.n_splits = pl.n_splits;
+  p.chunk = pl.chunk;
+  p.mask_mode = d->mask_mode;
+  p.mask_block = d->mask_block > 0 ? d->mask_block : 1;
+  p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
+  if (need > 0) {
+    char* w = static_cast<char*>(workspace);
+    p.ws_cnt = reinterpret_cast<int*>(w);
+    p.ws_ml = reinterpret_cast<float2*>(w + align256(pl.ws_cnt_bytes));
+    p.ws_o = reinterpret_cast<float*>(w + align256(pl.ws_cnt_bytes) + align256(pl.ws_ml_bytes));
+  } else {
+    p.ws_cnt = nullptr;
+    p.ws_ml = nullptr;
+    p.ws_o = nullptr;
+  }
+  const dim3 grid(pl.n_splits, pl.n_rb, static_cast<unsigned>(grid_z));
+  const bool f16 = d->dtype == FDLLM_DTYPE_F16;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (d->head_dim == 128) {
+    if (pl.MT == 1) launch_attn<128, 1>(p, f16, grid, s);
+    else if (pl.MT == 2) launch_attn<128, 2>(p, f16, grid, s);
+    else launch_attn<128, 4>(p, f16, grid, s);
+  } else {
+    if (pl.MT == 1) launch_attn<64, 1>(p, f16, grid, s);
+    else if (pl.MT == 2) launch_attn<64, 2>(p, f16, grid, s);
+    else launch_attn<64, 4>(p, f16, grid, s);
+  }
+  FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
+}
+
+extern "C" int fdllm_kv_cache_write(const void* k_new, const void* v_new,
+                                    int64_t new_stride_b, int64_t new_stride_s, int64_t new_stride_h,
+                                    void* k_cache, void* v_cache,
+                                    int64_t cache_stride_page, int64_t cache_stride_slot, int64_t cache_stride_h,
+                                    const int32_t* page_table, int32_t max_pages, int32_t page_size,
+                                    int32_t max_seqlen,
+                                    const int32_t* write_start, int32_t write_offset,
+                                    const int64_t* positions,
+                                    int batch, int num_tokens, int num_kv_heads, int head_dim,
+                                    int dtype, void* stream) {
+  using namespace fdllm;
+  FDLLM_CHECK_ARG(dtype == FDLLM_DTYPE_BF16 || dtype == FDLLM_DTYPE_F16,
+                  "fdllm_kv_cache_write: dtype %d unsupported (bf16 or fp16 only)", dtype);
+  FDLLM_CHECK_ARG(batch >= 0 && num_tokens >= 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 8 == 0,
+                  "fdllm_kv_cache_write: bad sizes");
+  if (static_cast<int64_t>(batch) * num_tokens == 0) return FDLLM_OK;
+  FDLLM_CHECK_ARG(k_new && v_new && k_cache && v_cache, "fdllm_kv_cache_write: null pointer");
+  FDLLM_CHECK_ARG(page_table == nullptr || (page_size > 0 && max_pages > 0),
+                  "fdllm_kv_cache_write: page table needs page_size > 0 and max_pages > 0");
+  FDLLM_CHECK_ARG(aligned16(k_new) && aligned16(v_new) && aligned16(k_cache) && aligned16(v_cache),
+                  "fdllm_kv_cache_write: pointers must be 16-byte aligned");
+  FDLLM_CHECK_ARG(new_stride_b % 8 == 0 && new_stride_s % 8 == 0 && new_stride_h % 8 == 0 &&
+                      cache_stride_page % 8 == 0 && cache_stride_slot % 8 == 0 && cache_stride_h % 8 == 0,
+                  "fdllm_kv_cache_write: strides must be multiples of 8 elements");
+  KVWriteArgs a;
+  a.k_new = static_cast<const uint16_t*>(k_new);
+  a.v_new = static_cast<const uint16_t*>(v_new);
+  a.n_sb = new_stride_b;
+  a.n_ss = new_stride_s;
+  a.n_sh = new_stride_h;
+  a.k_cache = static_cast<uint16_t*>(k_cache);
+  a.v_cache = static_cast<uint16_t*>(v_cache);
+  a.c_sp = cache_stride_page;
+  a.c_ss = cache_stride_slot;
+  a.c_sh = cache_stride_h;
+  a.page_table = page_table;
+  a.max_pages = max_pages;
+  a.page_size = page_size;
+  a.max_seqlen = max_seqlen;
+  a.write_start = write_start;
+  a.write_offset = write_offset;
+  a.positions = positions;
+  a.B = batch;
+  a.T = num_tokens;
+  a.Hkv = num_kv_heads;
+  a.D = head_dim;
+  const int64_t n = static_cast<int64_t>(batch) * num_tokens * num_kv_heads * (head_dim / 8);
+  kv_write_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(a);
+  FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_cache_write");
+}

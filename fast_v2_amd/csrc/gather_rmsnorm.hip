@@ -1,0 +1,475 @@
+// Row gather + RMSNorm and row scatter for gfx950.
+//
+// Semantics follow cuda_bench/fused_gather_norm.cu (select_gather_rmsnorm_kernel
+// :123-175, gather_rmsnorm_kernel :21-58, scatter_and_return_kernel :79-99) and
+// the RMSNorm rounding order of Fast_dLLM_QwenRMSNorm.forward (modeling.py:427-432).
+//
+// Design (HBM-bound, one pass over each selected row):
+//   - one 64-lane wavefront per output row; the row is pulled into registers
+//     with 16-byte loads (VPL loads per lane, all issued before any use),
+//   - sum of squares in fp32, reduced across the wave with DPP row moves plus
+//     two cross-row swizzles; no LDS, no atomics, deterministic order,
+//   - the gathered copy and the normalised row are written from the same
+//     registers, so each input byte is read exactly once.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "fdllm_common.h"
+
+namespace fdllm {
+
+namespace {
+
+// 16 bytes of T unpacked to fp32 and back.
+template <typename T>
+struct Vec16;
+template <>
+struct Vec16<bf16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void unpack(const u32x4& v, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = Elt<bf16_t>::lo(v[i]);
+      f[2 * i + 1] = Elt<bf16_t>::hi(v[i]);
+    }
+  }
+  __device__ __forceinline__ static u32x4 pack(const float* f) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = Elt<bf16_t>::pack(f[2 * i], f[2 * i + 1]);
+    return v;
+  }
+  __device__ __forceinline__ static float round(float x) { return Elt<bf16_t>::round(x); }
+};
+template <>
+struct Vec16<f16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void unpack(const u32x4& v, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f[2 * i] = Elt<f16_t>::lo(v[i]);
+      f[2 * i + 1] = Elt<f16_t>::hi(v[i]);
+    }
+  }
+  __device__ __forceinline__ static u32x4 pack(const float* f) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = Elt<f16_t>::pack(f[2 * i], f[2 * i + 1]);
+    return v;
+  }
+  __device__ __forceinline__ static float round(float x) { return Elt<f16_t>::round(x); }
+};
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void unpack(const u32x4& v, float* f) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = __uint_as_float(v[i]);
+  }
+  __device__ __forceinline__ static u32x4 pack(const float* f) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = __float_as_uint(f[i]);
+    return v;
+  }
+  __device__ __forceinline__ static float round(float x) { return x; }
+};
+
+// Load elements [e0, e0 + N) of the weight vector as fp32.
+template <int N>
+__device__ __forceinline__ void load_weight(const void* w, int wdtype, int e0, float* out) {
+  if (wdtype == FDLLM_DTYPE_F32) {
+    const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const float*>(w) + e0);
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      u32x4 v = p[i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) out[4 * i + j] = __uint_as_float(v[j]);
+    }
+  } else {
+    // 2-byte weights: N == 8 -> one 16-byte load, N == 4 -> one 8-byte load.
+    const uint16_t* base = static_cast<const uint16_t*>(w) + e0;
+    uint32_t words[N / 2];
+    if constexpr (N == 8) {
+      u32x4 v = *reinterpret_cast<const u32x4*>(base);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) words[j] = v[j];
+    } else {
+      u32x2 v = *reinterpret_cast<const u32x2*>(base);
+      words[0] = v[0];
+      words[1] = v[1];
+    }
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+      if (wdtype == FDLLM_DTYPE_BF16) {
+        out[2 * j] = Elt<bf16_t>::lo(words[j]);
+        out[2 * j + 1] = Elt<bf16_t>::hi(words[j]);
+      } else {
+        out[2 * j] = Elt<f16_t>::lo(words[j]);
+        out[2 * j + 1] = Elt<f16_t>::hi(words[j]);
+      }
+    }
+  }
+}
+
+__device__ __forceinline__ float load_weight_scalar(const void* w, int wdtype, int e) {
+  if (wdtype == FDLLM_DTYPE_F32) return static_cast<const float*>(w)[e];
+  const uint16_t bits = static_cast<const uint16_t*>(w)[e];
+  return wdtype == FDLLM_DTYPE_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
+}
+
+template <typename T>
+__device__ __forceinline__ float apply_norm(float x, float inv, float w, int mode) {
+  if (mode == FDLLM_NORM_PLAIN) return x * inv;
+  if (mode == FDLLM_NORM_WEIGHT_FP32) return (x * inv) * w;
+  // FDLLM_NORM_WEIGHT_AFTER_CAST: weight * normalized.to(dtype), product rounded once more
+  return w * Vec16<T>::round(x * inv);
+}
+
+struct GatherArgs {
+  const void* hidden;
+  int64_t hs_b, hs_s;
+  const int64_t* idx;
+  int64_t is_b;
+  const void* weight;
+  int wdtype;
+  void* normed;
+  void* gathered;
+  int B, S, T, H;
+  float eps;
+  int mode;
+};
+
+// Vector path: H * sizeof(T) is a multiple of 16 and every row is 16-byte aligned.
+// VPL = 16-byte vectors per lane (the whole row stays in registers).
+template <typename T, int VPL>
+__global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArgs a) {
+  constexpr int N = Vec16<T>::N;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= static_cast<int64_t>(a.B) * a.T) return;
+  const int b = static_cast<int>(row / a.T);
+  const int t = static_cast<int>(row - static_cast<int64_t>(b) * a.T);
+  const int nvec = a.H / N;
+  const int64_t src = a.idx[b * a.is_b + t];
+
+  u32x4* nrow = reinterpret_cast<u32x4*>(static_cast<T*>(a.normed) + row * a.H);
+  u32x4* grow = a.gathered ? reinterpret_cast<u32x4*>(static_cast<T*>(a.gathered) + row * a.H) : nullptr;
+
+  if (src < 0 || src >= a.S) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int c = lane + kWave * v;
+      if (c < nvec) {
+        nrow[c] = z;
+        if (grow) grow[c] = z;
+      }
+    }
+    return;
+  }
+
+  const u32x4* hrow = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.hidden) + b * a.hs_b + src * a.hs_s);
+  u32x4 x[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int c = lane + kWave * v;
+    if (c < nvec) {
+      x[v] = hrow[c];
+    } else {
+      x[v] = u32x4{0u, 0u, 0u, 0u};
+    }
+  }
+
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    float f[N];
+    Vec16<T>::unpack(x[v], f);
+#pragma unroll
+    for (int i = 0; i < N; ++i) ss += f[i] * f[i];
+  }
+  ss = wave_allreduce_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(a.H) + a.eps);
+
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int c = lane + kWave * v;
+    if (c < nvec) {
+      if (grow) grow[c] = x[v];
+      float f[N];
+      Vec16<T>::unpack(x[v], f);
+      float w[N];
+      if (a.mode != FDLLM_NORM_PLAIN) {
+        load_weight<N>(a.weight, a.wdtype, c * N, w);
+      } else {
+#pragma unroll
+        for (int i = 0; i < N; ++i) w[i] = 1.f;
+      }
+#pragma unroll
+      for (int i = 0; i < N; ++i) f[i] = apply_norm<T>(f[i], inv, w[i], a.mode);
+      nrow[c] = Vec16<T>::pack(f);
+    }
+  }
+}
+
+// Generic path: any H, any alignment. One wave per row, two passes over the row.
+template <typename T>
+__device__ __forceinline__ float load_elem(const T* p);
+template <>
+__device__ __forceinline__ float load_elem<float>(const float* p) { return *p; }
+template <>
+__device__ __forceinline__ float load_elem<bf16_t>(const bf16_t* p) { return bf16_bits_to_f32(p->bits); }
+template <>
+__device__ __forceinline__ float load_elem<f16_t>(const f16_t* p) { return f16_bits_to_f32(p->bits); }
+
+template <typename T>
+__device__ __forceinline__ void store_elem(T* p, float v);
+template <>
+__device__ __forceinline__ void store_elem<float>(float* p, float v) { *p = v; }
+template <>
+__device__ __forceinline__ void store_elem<bf16_t>(bf16_t* p, float v) { p->bits = static_cast<uint16_t>(f32_to_bf16_bits(v)); }
+template <>
+__device__ __forceinline__ void store_elem<f16_t>(f16_t* p, float v) { p->bits = static_cast<uint16_t>(f32_to_f16_bits(v)); }
+
+template <typename T>
+__global__ __launch_bounds__(256) void gather_rmsnorm_generic_kernel(const GatherArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= static_cast<int64_t>(a.B) * a.T) return;
+  const int b = static_cast<int>(row / a.T);
+  const int t = static_cast<int>(row - static_cast<int64_t>(b) * a.T);
+  const int64_t src = a.idx[b * a.is_b + t];
+  T* nrow = static_cast<T*>(a.normed) + row * a.H;
+  T* grow = a.gathered ? static_cast<T*>(a.gathered) + row * a.H : nullptr;
+  if (src < 0 || src >= a.S) {
+    for (int e = lane; e < a.H; e += kWave) {
+      store_elem<T>(nrow + e, 0.f);
+      if (grow) store_elem<T>(grow + e, 0.f);
+    }
+    return;
+  }
+  const T* hrow = static_cast<const T*>(a.hidden) + b * a.hs_b + src * a.hs_s;
+  float ss = 0.f;
+  for (int e = lane; e < a.H; e += kWave) {
+    const float x = load_elem<T>(hrow + e);
+    ss += x * x;
+  }
+  ss = wave_allreduce_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(a.H) + a.eps);
+  for (int e = lane; e < a.H; e += kWave) {
+    if (grow) grow[e] = hrow[e];
+    const float x = load_elem<T>(hrow + e);
+    const float w = a.mode != FDLLM_NORM_PLAIN ? load_weight_scalar(a.weight, a.wdtype, e) : 1.f;
+    store_elem<T>(nrow + e, apply_norm<T>(x, inv, w, a.mode));
+  }
+}
+
+
+// Row scatter to two destinations (scatter_and_return_kernel, fused_gather_norm.cu:79-99):
+// one wave per source row, 16-byte vectors when rows are aligned, else 2/4-byte elements.
+struct ScatterArgs {
+  const void* values;
+  const int64_t* idx;
+  int64_t is_b;
+  void* cache;
+  int64_t cs_b, cs_s;
+  void* cur;
+  int64_t us_b, us_s;
+  int B, S, T, H;  // H in elements
+  int esize;       // bytes per element
+  int vec16;       // rows are 16-byte aligned and H * esize % 16 == 0
+};
+
+__global__ __launch_bounds__(256) void scatter_rows_kernel(const ScatterArgs a) {
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= static_cast<int64_t>(a.B) * a.T) return;
+  const int b = static_cast<int>(row / a.T);
+  const int t = static_cast<int>(row - static_cast<int64_t>(b) * a.T);
+  const int64_t dst = a.idx[b * a.is_b + t];
+  if (dst < 0 || dst >= a.S) return;
+  const char* src = static_cast<const char*>(a.values) + row * a.H * a.esize;
+  char* c = static_cast<char*>(a.cache) + (b * a.cs_b + dst * a.cs_s) * a.esize;
+  char* u = static_cast<char*>(a.cur) + (b * a.us_b + dst * a.us_s) * a.esize;
+  if (a.vec16) {
+    const int nvec = a.H * a.esize / 16;
+    for (int i = lane; i < nvec; i += kWave) {
+      const u32x4 v = reinterpret_cast<const u32x4*>(src)[i];
+      reinterpret_cast<u32x4*>(c)[i] = v;
+      reinterpret_cast<u32x4*>(u)[i] = v;
+    }
+  } else if (a.esize == 4) {
+    for (int i = lane; i < a.H; i += kWave) {
+      const uint32_t v = reinterpret_cast<const uint32_t*>(src)[i];
+      reinterpret_cast<uint32_t*>(c)[i] = v;
+      reinterpret_cast<uint32_t*>(u)[i] = v;
+    }
+  } else {
+    for (int i = lane; i < a.H; i += kWave) {
+      const uint16_t v = reinterpret_cast<const uint16_t*>(src)[i];
+      reinterpret_cast<uint16_t*>(c)[i] = v;
+      reinterpret_cast<uint16_t*>(u)[i] = v;
+    }
+  }
+}
+
+template <typename T>
+int launch_gather(const GatherArgs& a, bool vec, hipStream_t stream) {
+  const int64_t rows = static_cast<int64_t>(a.B) * a.T;
+  const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
+  const dim3 block(256);
+  if (vec) {
+    const int nvec = a.H / Vec16<T>::N;
+    const int vpl = (nvec + kWave - 1) / kWave;
+    switch (vpl) {
+#define FDLLM_VPL_CASE(n) \
+  case n:                 \
+    gather_rmsnorm_vec_kernel<T, n><<<grid, block, 0, stream>>>(a); \
+    return 0;
+      FDLLM_VPL_CASE(1)
+      FDLLM_VPL_CASE(2)
+      FDLLM_VPL_CASE(3)
+      FDLLM_VPL_CASE(4)
+      FDLLM_VPL_CASE(5)
+      FDLLM_VPL_CASE(6)
+      FDLLM_VPL_CASE(7)
+      FDLLM_VPL_CASE(8)
+      FDLLM_VPL_CASE(10)
+      FDLLM_VPL_CASE(12)
+      FDLLM_VPL_CASE(14)
+      FDLLM_VPL_CASE(16)
+#undef FDLLM_VPL_CASE
+      default:
+        break;  // uneven or very wide rows: generic path
+    }
+  }
+  gather_rmsnorm_generic_kernel<T><<<grid, block, 0, stream>>>(a);
+  return 0;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace
+
+static thread_local char g_last_error[512];
+
+void set_last_error(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+}
+
+int dtype_size(int dtype) {
+  switch (dtype) {
+    case FDLLM_DTYPE_F32:
+      return 4;
+    case FDLLM_DTYPE_BF16:
+    case FDLLM_DTYPE_F16:
+      return 2;
+    default:
+      return 0;
+  }
+}
+
+}  // namespace fdllm
+
+extern "C" int fdllm_abi_version(void) { return FDLLM_ABI_VERSION; }
+
+extern "C" const char* fdllm_last_error(void) { return fdllm::g_last_error; }
+
+extern "C" int fdllm_gather_rmsnorm(const void* hidden, int64_t hidden_batch_stride, int64_t hidden_row_stride,
+                                    const int64_t* indices, int64_t indices_batch_stride,
+                                    const void* weight, int weight_dtype,
+                                    void* normed, void* gathered,
+                                    int batch, int seq_len, int num_tokens, int hidden_size,
+                                    float eps, int dtype, int norm_mode, void* stream) {
+  using namespace fdllm;
+  const int es = dtype_size(dtype);
+  FDLLM_CHECK_ARG(es != 0, "fdllm_gather_rmsnorm: unsupported dtype %d", dtype);
+  FDLLM_CHECK_ARG(norm_mode >= FDLLM_NORM_PLAIN && norm_mode <= FDLLM_NORM_WEIGHT_AFTER_CAST,
+                  "fdllm_gather_rmsnorm: unknown norm_mode %d", norm_mode);
+  FDLLM_CHECK_ARG(batch >= 0 && seq_len >= 0 && num_tokens >= 0 && hidden_size > 0,
+                  "fdllm_gather_rmsnorm: bad sizes B=%d S=%d T=%d H=%d", batch, seq_len, num_tokens, hidden_size);
+  if (static_cast<int64_t>(batch) * num_tokens == 0) return FDLLM_OK;
+  FDLLM_CHECK_ARG(hidden && indices && normed, "fdllm_gather_rmsnorm: null pointer");
+  FDLLM_CHECK_ARG(norm_mode == FDLLM_NORM_PLAIN || weight != nullptr,
+                  "fdllm_gather_rmsnorm: norm_mode %d needs a weight", norm_mode);
+  FDLLM_CHECK_ARG(norm_mode == FDLLM_NORM_PLAIN || dtype_size(weight_dtype) != 0,
+                  "fdllm_gather_rmsnorm: unsupported weight dtype %d", weight_dtype);
+  FDLLM_CHECK_ARG(!(eps < 0.f), "fdllm_gather_rmsnorm: eps must be >= 0");
+
+  GatherArgs a;
+  a.hidden = hidden;
+  a.hs_b = hidden_batch_stride;
+  a.hs_s = hidden_row_stride;
+  a.idx = indices;
+  a.is_b = indices_batch_stride;
+  a.weight = weight;
+  a.wdtype = weight_dtype;
+  a.normed = normed;
+  a.gathered = gathered;
+  a.B = batch;
+  a.S = seq_len;
+  a.T = num_tokens;
+  a.H = hidden_size;
+  a.eps = eps;
+  a.mode = norm_mode;
+
+  const int N = 16 / es;
+  const int wsz = norm_mode == FDLLM_NORM_PLAIN ? 0 : dtype_size(weight_dtype);
+  const bool vec = (hidden_size % N == 0) && aligned16(hidden) && aligned16(normed) &&
+                   (gathered == nullptr || aligned16(gathered)) &&
+                   ((hidden_batch_stride * es) % 16 == 0) && ((hidden_row_stride * es) % 16 == 0) &&
+                   (wsz == 0 || (reinterpret_cast<uintptr_t>(weight) % (wsz * N < 16 ? wsz * N : 16)) == 0);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case FDLLM_DTYPE_BF16:
+      launch_gather<bf16_t>(a, vec, s);
+      break;
+    case FDLLM_DTYPE_F16:
+      launch_gather<f16_t>(a, vec, s);
+      break;
+    default:
+      launch_gather<float>(a, vec, s);
+      break;
+  }
+  FDLLM_RETURN_LAUNCH_STATUS("fdllm_gather_rmsnorm");
+}
+
+extern "C" int fdllm_scatter_rows(const void* values, const int64_t* indices, int64_t indices_batch_stride,
+                                  void* cache, int64_t cache_batch_stride, int64_t cache_row_stride,
+                                  void* current, int64_t current_batch_stride, int64_t current_row_stride,
+                                  int batch, int seq_len, int num_tokens, int hidden_size,
+                                  int dtype, void* stream) {
+  using namespace fdllm;
+  const int es = dtype_size(dtype);
+  FDLLM_CHECK_ARG(es != 0, "fdllm_scatter_rows: unsupported dtype %d", dtype);
+  FDLLM_CHECK_ARG(batch >= 0 && seq_len >= 0 && num_tokens >= 0 && hidden_size > 0,
+                  "fdllm_scatter_rows: bad sizes B=%d S=%d T=%d H=%d", batch, seq_len, num_tokens, hidden_size);
+  if (static_cast<int64_t>(batch) * num_tokens == 0) return FDLLM_OK;
+  FDLLM_CHECK_ARG(values && indices && cache && current, "fdllm_scatter_rows: null pointer");
+  ScatterArgs a;
+  a.values = values;
+  a.idx = indices;
+  a.is_b = indices_batch_stride;
+  a.cache = cache;
+  a.cs_b = cache_batch_stride;
+  a.cs_s = cache_row_stride;
+  a.cur = current;
+  a.us_b = current_batch_stride;
+  a.us_s = current_row_stride;
+  a.B = batch;
+  a.S = seq_len;
+  a.T = num_tokens;
+  a.H = hidden_size;
+  a.esize = es;
+  a.vec16 = ((static_cast<int64_t>(hidden_size) * es) % 16 == 0) && aligned16(values) && aligned16(cache) &&
+            aligned16(current) && (cache_batch_stride * es) % 16 == 0 && (cache_row_stride * es) % 16 == 0 &&
+            (current_batch_stride * es) % 16 == 0 && (current_row_stride * es) % 16 == 0;
+  const int64_t rows = static_cast<int64_t>(batch) * num_tokens;
+  scatter_rows_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
+                        static_cast<hipStream_t>(stream)>>>(a);
+  FDLLM_RETURN_LAUNCH_STATUS("fdllm_scatter_rows");
+}

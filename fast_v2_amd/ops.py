@@ -1,0 +1,376 @@
+"""Tensor-level entry points over libfdllm_hip.so, plus their torch.library ops.
+
+Every function here validates its tensors, allocates the outputs with torch
+(on the tensors' device, on the current stream) and launches the HIP kernel
+through the C ABI. Nothing here computes on the CPU: CPU tensors, unsupported
+dtypes or a missing library raise ``RuntimeError``.
+
+torch.library ops (namespace ``fdllm``), each with a Meta implementation so
+that graph capture / FakeTensor tracing can infer output shapes without data,
+in the manner of ``_wrap_flash_kvcache_as_custom_op``
+(utils/attention_backends.py:73-120):
+
+    fdllm::flash_kvcache(Tensor q, Tensor k_cache, Tensor v_cache,
+                         Tensor cache_seqlens, float softmax_scale, bool causal) -> Tensor
+    fdllm::block_attn(Tensor q, Tensor k_cache, Tensor v_cache, Tensor cache_seqlens,
+                      float softmax_scale, int mask_mode, int mask_block,
+                      Tensor? q_start, Tensor? page_table, int page_size) -> Tensor
+    fdllm::gather_rmsnorm(Tensor hidden, Tensor indices, Tensor? weight, float eps,
+                          int norm_mode, bool with_gathered) -> (Tensor, Tensor)
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+from typing import Optional, Tuple
+
+import torch
+
+from . import _ffi
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+def _require_gpu(*tensors: torch.Tensor) -> torch.device:
+    dev = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise RuntimeError(
+                f"libfdllm_hip kernels need GPU tensors; got a tensor on {t.device}")
+        if t.device != dev:
+            raise RuntimeError(f"tensors on different devices: {dev} vs {t.device}")
+    return dev
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+class _Workspace:
+    """Zero-filled scratch per (device, stream), grown on demand and reused.
+
+    The split-KV attention leaves its workspace ready for the next call (its
+    completion counters are re-armed by the kernel), so the buffer is cleared
+    only when it is first allocated.
+    """
+
+    def __init__(self) -> None:
+        self._bufs: dict = {}
+
+    def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
+        stream = torch.cuda.current_stream(device)
+        key = (device.index, stream.cuda_stream)
+        buf = self._bufs.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            self._bufs[key] = buf
+        return buf
+
+
+_WORKSPACE = _Workspace()
+
+
+# ---------------------------------------------------------------------------
+# gather + RMSNorm / scatter
+# ---------------------------------------------------------------------------
+
+def gather_rmsnorm(
+    hidden: torch.Tensor,
+    indices: torch.Tensor,
+    weight: Optional[torch.Tensor],
+    eps: float,
+    norm_mode: int = _ffi.NORM_WEIGHT_AFTER_CAST,
+    with_gathered: bool = True,
+) -> Tuple[torch.Tensor, Optional[torch.Tensor]]:
+    """Gather rows ``hidden[b, indices[b, t]]`` and RMS-normalise them in one pass.
+
+    hidden  [B, S, H] (last dim contiguous), bf16 / fp16 / fp32
+    indices [B, T] integer (int64 used as is, other integer types converted)
+    weight  [H] or None (then norm_mode must be NORM_PLAIN)
+    Returns (normed [B, T, H], gathered [B, T, H] or None), both in hidden's dtype.
+    """
+    if hidden.dim() != 3 or indices.dim() != 2 or indices.shape[0] != hidden.shape[0]:
+        raise RuntimeError(
+            f"gather_rmsnorm: expected hidden [B,S,H] and indices [B,T]; got "
+            f"{tuple(hidden.shape)} and {tuple(indices.shape)}")
+    dev = _require_gpu(hidden, indices, *([weight] if weight is not None else []))
+    if hidden.stride(-1) != 1:
+        hidden = hidden.contiguous()
+    if indices.dtype != torch.int64 or indices.stride(-1) != 1:
+        indices = indices.to(torch.int64).contiguous()
+    if weight is not None:
+        weight = weight.contiguous()
+        if weight.numel() != hidden.shape[-1]:
+            raise RuntimeError("gather_rmsnorm: weight size must equal hidden size")
+    elif norm_mode != _ffi.NORM_PLAIN:
+        raise RuntimeError("gather_rmsnorm: this norm_mode needs a weight")
+    B, S, H = hidden.shape
+    T = indices.shape[1]
+    normed = torch.empty((B, T, H), dtype=hidden.dtype, device=dev)
+    gathered = torch.empty((B, T, H), dtype=hidden.dtype, device=dev) if with_gathered else None
+    rc = _ffi.lib().fdllm_gather_rmsnorm(
+        hidden.data_ptr(), hidden.stride(0), hidden.stride(1),
+        indices.data_ptr(), indices.stride(0),
+        _ptr(weight), _ffi.dtype_code(weight.dtype) if weight is not None else 0,
+        normed.data_ptr(), _ptr(gathered),
+        B, S, T, H, float(eps), _ffi.dtype_code(hidden.dtype), int(norm_mode),
+        _ffi.stream_ptr(dev))
+    _ffi.check(rc, "fdllm_gather_rmsnorm")
+    return normed, gathered
+
+
+def scatter_rows(values: torch.Tensor, indices: torch.Tensor,
+                 cache: torch.Tensor, current: torch.Tensor) -> torch.Tensor:
+    """cache[b, indices[b,t]] = current[b, indices[b,t]] = values[b, t]; returns ``current``."""
+    if values.dim() != 3 or cache.dim() != 3 or current.dim() != 3 or indices.dim() != 2:
+        raise RuntimeError("scatter_rows: expected values/cache/current [B,*,H] and indices [B,T]")
+    dev = _require_gpu(values, indices, cache, current)
+    if cache.dtype != values.dtype or current.dtype != values.dtype:
+        raise RuntimeError("scatter_rows: values, cache and current must share a dtype")
+    if cache.shape != current.shape or cache.shape[0] != values.shape[0] or cache.shape[2] != values.shape[2]:
+        raise RuntimeError("scatter_rows: shape mismatch")
+    if cache.stride(-1) != 1 or current.stride(-1) != 1:
+        raise RuntimeError("scatter_rows: cache/current last dim must be contiguous (written in place)")
+    values = values.contiguous()
+    if indices.dtype != torch.int64 or indices.stride(-1) != 1:
+        indices = indices.to(torch.int64).contiguous()
+    B, T, H = values.shape
+    S = cache.shape[1]
+    rc = _ffi.lib().fdllm_scatter_rows(
+        values.data_ptr(), indices.data_ptr(), indices.stride(0),
+        cache.data_ptr(), cache.stride(0), cache.stride(1),
+        current.data_ptr(), current.stride(0), current.stride(1),
+        B, S, T, H, _ffi.dtype_code(values.dtype), _ffi.stream_ptr(dev))
+    _ffi.check(rc, "fdllm_scatter_rows")
+    return current
+
+
+# ---------------------------------------------------------------------------
+# attention
+# ---------------------------------------------------------------------------
+
+def _attn_desc(q, k_cache, v_cache, seqlens, out, scale, mask_mode, mask_block,
+               q_start, page_table, page_size, kv_split) -> _ffi.KVAttnDesc:
+    B, Sq, Hq, D = q.shape
+    d = _ffi.KVAttnDesc()
+    d.q = q.data_ptr()
+    d.q_stride_b, d.q_stride_s, d.q_stride_h = q.stride(0), q.stride(1), q.stride(2)
+    d.k = k_cache.data_ptr()
+    d.k_stride_page, d.k_stride_slot, d.k_stride_h = k_cache.stride(0), k_cache.stride(1), k_cache.stride(2)
+    d.v = v_cache.data_ptr()
+    d.v_stride_page, d.v_stride_slot, d.v_stride_h = v_cache.stride(0), v_cache.stride(1), v_cache.stride(2)
+    d.out = out.data_ptr()
+    d.out_stride_b, d.out_stride_s, d.out_stride_h = out.stride(0), out.stride(1), out.stride(2)
+    d.seqlens = seqlens.data_ptr()
+    d.q_start = _ptr(q_start)
+    if page_table is not None:
+        d.page_table = page_table.data_ptr()
+        d.max_pages = page_table.shape[1]
+        d.page_size = int(page_size)
+        d.max_seqlen = page_table.shape[1] * int(page_size)
+    else:
+        d.page_table = None
+        d.max_pages = 0
+        d.page_size = 0
+        d.max_seqlen = k_cache.shape[1]
+    d.batch, d.q_len, d.num_q_heads, d.num_kv_heads, d.head_dim = B, Sq, Hq, k_cache.shape[2], D
+    d.mask_mode = int(mask_mode)
+    d.mask_block = int(mask_block)
+    d.dtype = _ffi.dtype_code(q.dtype)
+    d.kv_split = int(kv_split)
+    d.softmax_scale = float(scale)
+    return d
+
+
+def block_attn(
+    q: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    cache_seqlens: torch.Tensor,
+    softmax_scale: Optional[float] = None,
+    mask_mode: int = _ffi.MASK_SEQLEN,
+    mask_block: int = 32,
+    q_start: Optional[torch.Tensor] = None,
+    page_table: Optional[torch.Tensor] = None,
+    page_size: int = 0,
+    out: Optional[torch.Tensor] = None,
+    kv_split: int = 0,
+) -> torch.Tensor:
+    """Attention of BSHD queries over a (paged) BSHD KV cache.
+
+    q            [B, Sq, Hq, D] bf16/fp16 (head_dim contiguous)
+    k/v_cache    [B, max_S, Hkv, D] without a page table, or the page pool
+                 [num_pages, page_size, Hkv, D] with ``page_table`` [B, max_pages] int32
+    cache_seqlens [B] visible key count per sequence (int32; other ints converted)
+    Returns a new [B, Sq, Hq, D] tensor (or fills ``out``).
+    """
+    if q.dim() != 4 or k_cache.dim() != 4 or v_cache.dim() != 4:
+        raise RuntimeError("block_attn: q, k_cache and v_cache must be 4-D (BSHD)")
+    tensors = [q, k_cache, v_cache, cache_seqlens]
+    if q_start is not None:
+        tensors.append(q_start)
+    if page_table is not None:
+        tensors.append(page_table)
+    dev = _require_gpu(*tensors)
+    if not (q.dtype == k_cache.dtype == v_cache.dtype) or q.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError(
+            f"block_attn: q/k/v must share dtype bf16 or fp16 (got {q.dtype}, {k_cache.dtype}, {v_cache.dtype})")
+    if k_cache.shape != v_cache.shape:
+        raise RuntimeError("block_attn: k_cache and v_cache shapes differ")
+    B, Sq, Hq, D = q.shape
+    if k_cache.shape[3] != D:
+        raise RuntimeError("block_attn: head_dim mismatch between q and the cache")
+    if Hq % k_cache.shape[2] != 0:
+        raise RuntimeError("block_attn: num_q_heads must be a multiple of num_kv_heads")
+    if page_table is None and k_cache.shape[0] != B:
+        raise RuntimeError("block_attn: cache batch dim must equal q batch dim without a page table")
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if k_cache.stride(-1) != 1 or v_cache.stride(-1) != 1:
+        raise RuntimeError("block_attn: cache head_dim must be contiguous")
+    if cache_seqlens.dtype != torch.int32 or not cache_seqlens.is_contiguous():
+        cache_seqlens = cache_seqlens.to(torch.int32).contiguous()
+    if q_start is not None and (q_start.dtype != torch.int32 or not q_start.is_contiguous()):
+        q_start = q_start.to(torch.int32).contiguous()
+    if page_table is not None:
+        if page_table.dtype != torch.int32 or not page_table.is_contiguous():
+            page_table = page_table.to(torch.int32).contiguous()
+        if page_size <= 0 or k_cache.shape[1] != page_size:
+            raise RuntimeError("block_attn: page pool dim 1 must equal page_size")
+    if out is None:
+        out = torch.empty((B, Sq, Hq, D), dtype=q.dtype, device=dev)
+    elif out.shape != (B, Sq, Hq, D) or out.dtype != q.dtype or out.stride(-1) != 1:
+        raise RuntimeError("block_attn: bad `out` tensor")
+    if softmax_scale is None:
+        softmax_scale = D ** -0.5
+    desc = _attn_desc(q, k_cache, v_cache, cache_seqlens, out, softmax_scale, mask_mode,
+                      mask_block, q_start, page_table, page_size, kv_split)
+    L = _ffi.lib()
+    need = ctypes.c_size_t(0)
+    _ffi.check(L.fdllm_kv_attn_workspace_size(ctypes.byref(desc), ctypes.byref(need)),
+               "fdllm_kv_attn_workspace_size")
+    ws_ptr, ws_bytes = None, 0
+    if need.value:
+        ws = _WORKSPACE.get(need.value, dev)
+        ws_ptr, ws_bytes = ws.data_ptr(), ws.numel()
+    rc = L.fdllm_kv_attn_fwd(ctypes.byref(desc), ws_ptr, ws_bytes, _ffi.stream_ptr(dev))
+    _ffi.check(rc, "fdllm_kv_attn_fwd")
+    return out
+
+
+def kv_cache_write(
+    k_new: torch.Tensor,
+    v_new: torch.Tensor,
+    k_cache: torch.Tensor,
+    v_cache: torch.Tensor,
+    write_offset: int = 0,
+    write_start: Optional[torch.Tensor] = None,
+    positions: Optional[torch.Tensor] = None,
+    page_table: Optional[torch.Tensor] = None,
+    page_size: int = 0,
+) -> None:
+    """Write new BSHD K/V rows [B, T, Hkv, D] into the cache in place.
+
+    Row t of sequence b goes to position ``positions[b, t]`` if given, else
+    ``write_start[b] + t`` if given, else ``write_offset + t``.
+    """
+    if k_new.dim() != 4 or k_new.shape != v_new.shape:
+        raise RuntimeError("kv_cache_write: k_new / v_new must be matching [B, T, Hkv, D]")
+    tensors = [k_new, v_new, k_cache, v_cache]
+    for t in (write_start, positions, page_table):
+        if t is not None:
+            tensors.append(t)
+    dev = _require_gpu(*tensors)
+    if not (k_new.dtype == v_new.dtype == k_cache.dtype == v_cache.dtype):
+        raise RuntimeError("kv_cache_write: dtype mismatch")
+    if k_cache.shape != v_cache.shape or k_cache.stride() != v_cache.stride():
+        raise RuntimeError("kv_cache_write: k_cache and v_cache must have the same shape and strides")
+    B, T, Hkv, D = k_new.shape
+    if k_cache.shape[2] != Hkv or k_cache.shape[3] != D or k_cache.stride(-1) != 1:
+        raise RuntimeError("kv_cache_write: cache shape mismatch")
+    if page_table is None and k_cache.shape[0] != B:
+        raise RuntimeError("kv_cache_write: cache batch dim must equal the batch without a page table")
+    if k_new.stride() != v_new.stride() or k_new.stride(-1) != 1:
+        k_new = k_new.contiguous()
+        v_new = v_new.contiguous()
+    if write_start is not None and (write_start.dtype != torch.int32 or not write_start.is_contiguous()):
+        write_start = write_start.to(torch.int32).contiguous()
+    if positions is not None and (positions.dtype != torch.int64 or not positions.is_contiguous()):
+        positions = positions.to(torch.int64).contiguous()
+    if page_table is not None and (page_table.dtype != torch.int32 or not page_table.is_contiguous()):
+        page_table = page_table.to(torch.int32).contiguous()
+    rc = _ffi.lib().fdllm_kv_cache_write(
+        k_new.data_ptr(), v_new.data_ptr(), k_new.stride(0), k_new.stride(1), k_new.stride(2),
+        k_cache.data_ptr(), v_cache.data_ptr(), k_cache.stride(0), k_cache.stride(1), k_cache.stride(2),
+        _ptr(page_table), page_table.shape[1] if page_table is not None else 0, int(page_size),
+        k_cache.shape[1] if page_table is None else page_table.shape[1] * int(page_size),
+        _ptr(write_start), int(write_offset), _ptr(positions),
+        B, T, Hkv, D, _ffi.dtype_code(k_new.dtype), _ffi.stream_ptr(dev))
+    _ffi.check(rc, "fdllm_kv_cache_write")
+
+
+# ---------------------------------------------------------------------------
+# torch.library registration
+# ---------------------------------------------------------------------------
+
+_LIB = torch.library.Library("fdllm", "DEF")
+_LIB.define(
+    "flash_kvcache(Tensor q, Tensor k_cache, Tensor v_cache, Tensor cache_seqlens, "
+    "float softmax_scale, bool causal) -> Tensor")
+_LIB.define(
+    "block_attn(Tensor q, Tensor k_cache, Tensor v_cache, Tensor cache_seqlens, "
+    "float softmax_scale, int mask_mode, int mask_block, Tensor? q_start, "
+    "Tensor? page_table, int page_size) -> Tensor")
+_LIB.define(
+    "gather_rmsnorm(Tensor hidden, Tensor indices, Tensor? weight, float eps, "
+    "int norm_mode, bool with_gathered) -> (Tensor, Tensor)")
+
+
+def _flash_kvcache_impl(q, k_cache, v_cache, cache_seqlens, softmax_scale, causal):
+    # causal=True follows flash_attn_with_kvcache: the mask is aligned to the
+    # bottom-right corner, i.e. query i sits at position seqlen - Sq + i.
+    mode = _ffi.MASK_CAUSAL if causal else _ffi.MASK_SEQLEN
+    return block_attn(q, k_cache, v_cache, cache_seqlens, softmax_scale, mask_mode=mode)
+
+
+def _flash_kvcache_meta(q, k_cache, v_cache, cache_seqlens, softmax_scale, causal):
+    return torch.empty_like(q)
+
+
+def _block_attn_impl(q, k_cache, v_cache, cache_seqlens, softmax_scale, mask_mode, mask_block,
+                     q_start, page_table, page_size):
+    return block_attn(q, k_cache, v_cache, cache_seqlens, softmax_scale, mask_mode, mask_block,
+                      q_start, page_table, page_size)
+
+
+def _block_attn_meta(q, k_cache, v_cache, cache_seqlens, softmax_scale, mask_mode, mask_block,
+                     q_start, page_table, page_size):
+    return torch.empty_like(q)
+
+
+def _gather_rmsnorm_impl(hidden, indices, weight, eps, norm_mode, with_gathered):
+    normed, gathered = gather_rmsnorm(hidden, indices, weight, eps, norm_mode, with_gathered)
+    if gathered is None:
+        gathered = hidden.new_empty((0,))
+    return normed, gathered
+
+
+def _gather_rmsnorm_meta(hidden, indices, weight, eps, norm_mode, with_gathered):
+    B, _, H = hidden.shape
+    T = indices.shape[1]
+    normed = hidden.new_empty((B, T, H))
+    gathered = hidden.new_empty((B, T, H)) if with_gathered else hidden.new_empty((0,))
+    return normed, gathered
+
+
+_LIB.impl("flash_kvcache", _flash_kvcache_impl, "CUDA")
+_LIB.impl("flash_kvcache", _flash_kvcache_meta, "Meta")
+_LIB.impl("block_attn", _block_attn_impl, "CUDA")
+_LIB.impl("block_attn", _block_attn_meta, "Meta")
+_LIB.impl("gather_rmsnorm", _gather_rmsnorm_impl, "CUDA")
+_LIB.impl("gather_rmsnorm", _gather_rmsnorm_meta, "Meta")
+
+flash_kvcache = torch.ops.fdllm.flash_kvcache
+
+LOG2E = 1.0 / math.log(2.0)

@@ -1,0 +1,198 @@
+/*
+ * libfdllm_hip.so — C ABI of the MI355X (gfx950) block-diffusion hot path.
+ *
+ * Two operator families, each a drop-in for one surface of navneet-13/fast_v2:
+ *
+ *   1. Row gather + RMSNorm (and the sibling row scatter), replacing the
+ *      pybind entry points of cuda_bench/fused_gather_norm.cu:215-221.
+ *   2. Block attention over the static / paged block KV cache, replacing the
+ *      flash_attn_with_kvcache call behind
+ *      AttentionBackend.flash_kvcache_attention (utils/attention_backends.py:588-640)
+ *      and the eager block-causal SDPA of the prefill/commit forward
+ *      (modeling.py:385-411 with eval_block_diff_mask, modeling.py:145-150).
+ *
+ * Conventions shared by every entry point:
+ *   - Plain device pointers, element strides and sizes; no framework types.
+ *   - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *     Every launch is asynchronous on that stream; no entry point synchronises
+ *     the host or allocates device memory.
+ *   - Return value: FDLLM_OK (0) on success, a negative FDLLM_ERR_* for a
+ *     rejected argument (nothing was launched), or a positive hipError_t when
+ *     the launch itself failed. fdllm_last_error() describes the last failure
+ *     of the calling thread.
+ *   - The last dimension of every tensor is contiguous (stride 1).
+ */
+#ifndef FDLLM_HIP_H_
+#define FDLLM_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+#define FDLLM_OK 0
+#define FDLLM_ERR_INVALID_ARGUMENT (-1)
+#define FDLLM_ERR_UNSUPPORTED (-2)
+#define FDLLM_ERR_WORKSPACE (-3)
+
+/* ---- element types ------------------------------------------------------ */
+#define FDLLM_DTYPE_F32 0
+#define FDLLM_DTYPE_BF16 1
+#define FDLLM_DTYPE_F16 2
+
+/* ---- how the RMSNorm weight is applied ---------------------------------- */
+/* out = x * rsqrt(mean(x^2) + eps)               (fused_gather_norm.cu:166-174, weight == nullptr) */
+#define FDLLM_NORM_PLAIN 0
+/* out = (x * rsqrt(mean(x^2) + eps)) * w, in fp32, one rounding  (fused_gather_norm.cu:53-57) */
+#define FDLLM_NORM_WEIGHT_FP32 1
+/* out = w * to_dtype(x * rsqrt(mean(x^2) + eps)), the Fast_dLLM_QwenRMSNorm
+ * order (modeling.py:427-432; fused_sparse_extension.py:80-87)                    */
+#define FDLLM_NORM_WEIGHT_AFTER_CAST 2
+
+/* ---- attention masks ---------------------------------------------------- */
+/* key j visible iff j < seqlens[b]  (flash_attn_with_kvcache, causal=False;
+ * the seqused mask of static_kv_cache.py:295-302)                               */
+#define FDLLM_MASK_SEQLEN 0
+/* key j visible iff j < seqlens[b] and j <= qpos(i)  (causal, query i at
+ * absolute position qpos(i) = q_start[b] + i)                                    */
+#define FDLLM_MASK_CAUSAL 1
+/* key j visible iff j < seqlens[b] and j / mask_block <= qpos(i) / mask_block
+ * (eval_block_diff_mask, modeling.py:145-150)                                    */
+#define FDLLM_MASK_BLOCK_CAUSAL 2
+
+/* Library identification: returns FDLLM_ABI_VERSION. */
+#define FDLLM_ABI_VERSION 1
+int fdllm_abi_version(void);
+
+/* Human-readable description of the calling thread's last failure ("" if none). */
+const char* fdllm_last_error(void);
+
+/* -------------------------------------------------------------------------
+ * Row gather + RMSNorm.
+ *
+ *   for b < batch, t < num_tokens:
+ *     s = indices[b * indices_batch_stride + t]
+ *     x = hidden[b * hidden_batch_stride + s * hidden_row_stride + 0 .. hidden_size)
+ *     gathered[b, t, :] = x                                  (bit-exact; optional)
+ *     normed[b, t, :]   = rmsnorm(x) per norm_mode, fp32 arithmetic
+ *
+ * hidden / normed / gathered share `dtype`; weight has `weight_dtype` and may be
+ * NULL only with FDLLM_NORM_PLAIN. normed and gathered are contiguous
+ * [batch, num_tokens, hidden_size]. An index outside [0, seq_len) yields a zero
+ * row in both outputs (the input is never read out of bounds).
+ *
+ * Replaces: gather_rmsnorm_cuda (fused_gather_norm.cu:60-73, NORM_WEIGHT_FP32),
+ * fused_select_norm (:177-190, NORM_WEIGHT_FP32),
+ * fused_gather_input_rmsnorm_pair (:193-209, NORM_PLAIN + gathered), and the
+ * model-path wrapper fused_sparse_extension.fused_gather_input_rmsnorm_pair
+ * (fused_sparse_extension.py:51-87, NORM_WEIGHT_AFTER_CAST + gathered).
+ * ------------------------------------------------------------------------- */
+int fdllm_gather_rmsnorm(const void* hidden, int64_t hidden_batch_stride, int64_t hidden_row_stride,
+                         const int64_t* indices, int64_t indices_batch_stride,
+                         const void* weight, int weight_dtype,
+                         void* normed, void* gathered,
+                         int batch, int seq_len, int num_tokens, int hidden_size,
+                         float eps, int dtype, int norm_mode, void* stream);
+
+/* -------------------------------------------------------------------------
+ * Row scatter to two destinations.
+ *
+ *   for b < batch, t < num_tokens:
+ *     s = indices[b * indices_batch_stride + t]
+ *     cache[b, s, :] = current[b, s, :] = values[b, t, :]
+ *
+ * values is contiguous [batch, num_tokens, hidden_size]; cache and current are
+ * [batch, seq_len, hidden_size] with the given strides. Out-of-range indices
+ * are skipped. Duplicate indices within a row race, as in the reference.
+ *
+ * Replaces: scatter_and_return_cuda (fused_gather_norm.cu:79-119).
+ * ------------------------------------------------------------------------- */
+int fdllm_scatter_rows(const void* values, const int64_t* indices, int64_t indices_batch_stride,
+                       void* cache, int64_t cache_batch_stride, int64_t cache_row_stride,
+                       void* current, int64_t current_batch_stride, int64_t current_row_stride,
+                       int batch, int seq_len, int num_tokens, int hidden_size,
+                       int dtype, void* stream);
+
+/* -------------------------------------------------------------------------
+ * Block attention over a (paged) KV cache.
+ *
+ * Query row (b, i, h) attends to the keys j of sequence b that the mask allows,
+ * using KV head h / (num_q_heads / num_kv_heads) (GQA), with
+ *   out = softmax(q . k^T * softmax_scale) . v      (fp32 softmax and accumulation)
+ * A row with no visible key produces zeros.
+ *
+ * KV addressing: element (j, kv_head, d) of sequence b lives at
+ *   base + page * stride_page + slot * stride_slot + kv_head * stride_head + d
+ * with (page, slot) = (page_table[b * max_pages + j / page_size], j % page_size)
+ * when page_table != NULL, else (b, j): the contiguous [batch, max_S, Hkv, D]
+ * static cache of static_kv_cache.py:55-69 is the page-table-free case.
+ * ------------------------------------------------------------------------- */
+typedef struct fdllm_kv_attn_desc {
+  const void* q; /* [batch, q_len, num_q_heads, head_dim] */
+  int64_t q_stride_b, q_stride_s, q_stride_h;
+  const void* k; /* key pool */
+  int64_t k_stride_page, k_stride_slot, k_stride_h;
+  const void* v; /* value pool */
+  int64_t v_stride_page, v_stride_slot, v_stride_h;
+  void* out; /* [batch, q_len, num_q_heads, head_dim] */
+  int64_t out_stride_b, out_stride_s, out_stride_h;
+  const int32_t* page_table; /* [batch, max_pages] or NULL */
+  const int32_t* seqlens;    /* [batch] visible KV length */
+  const int32_t* q_start;    /* [batch] absolute position of query 0, or NULL: seqlens[b] - q_len */
+  int32_t max_pages;         /* page-table row length (ignored without a page table) */
+  int32_t page_size;         /* tokens per page (ignored without a page table) */
+  int32_t max_seqlen;        /* upper bound on every seqlens[b]; sizes the grid */
+  int32_t batch, q_len, num_q_heads, num_kv_heads, head_dim;
+  int32_t mask_mode;  /* FDLLM_MASK_* */
+  int32_t mask_block; /* block length for FDLLM_MASK_BLOCK_CAUSAL */
+  int32_t dtype;      /* FDLLM_DTYPE_BF16 or FDLLM_DTYPE_F16 (q, k, v, out) */
+  int32_t kv_split;   /* keys per split-KV work item (multiple of 64), 0 = automatic */
+  float softmax_scale;
+} fdllm_kv_attn_desc;
+
+/* Bytes of device workspace fdllm_kv_attn_fwd needs for `desc` (0 when the call
+ * is not split over several workgroups per KV head). The first 16 KiB of the
+ * workspace hold split-completion counters: zero-fill the workspace once when it
+ * is allocated; every completed call leaves those counters at zero again, so one
+ * workspace serves any sequence of calls of any sizes. Calls that may overlap in
+ * time (different streams) need separate workspaces. */
+int fdllm_kv_attn_workspace_size(const fdllm_kv_attn_desc* desc, size_t* bytes);
+
+/* Launch the attention described by `desc` on `stream`. */
+int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* desc, void* workspace, size_t workspace_bytes,
+                      void* stream);
+
+/* -------------------------------------------------------------------------
+ * KV cache write: copy `num_tokens` new key/value rows of every sequence into
+ * the (paged) cache at positions write_start[b] + t (or `write_offset` + t when
+ * write_start is NULL).
+ *
+ *   k_cache[b, pos, h, :] = k_new[b, t, h, :];  v_cache likewise
+ *
+ * Positions are mapped to (page, slot) exactly as in fdllm_kv_attn_fwd.
+ * Positions at or beyond max_pages * page_size (or max_seqlen without a page
+ * table) are skipped.
+ *
+ * Replaces: StaticKVCache.update (static_kv_cache.py:132-160),
+ * write_scratch_compiled (:218-229) and write_sparse (:231-247, with
+ * `positions` = per-token absolute positions [batch, num_tokens]).
+ * ------------------------------------------------------------------------- */
+int fdllm_kv_cache_write(const void* k_new, const void* v_new,
+                         int64_t new_stride_b, int64_t new_stride_s, int64_t new_stride_h,
+                         void* k_cache, void* v_cache,
+                         int64_t cache_stride_page, int64_t cache_stride_slot, int64_t cache_stride_h,
+                         const int32_t* page_table, int32_t max_pages, int32_t page_size,
+                         int32_t max_seqlen,
+                         const int32_t* write_start, int32_t write_offset,
+                         const int64_t* positions,
+                         int batch, int num_tokens, int num_kv_heads, int head_dim,
+                         int dtype, void* stream);
+
+#ifdef __cplusplus
+} /* extern "C" */
+#endif
+
+#endif /* FDLLM_HIP_H_ */

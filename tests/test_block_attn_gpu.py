@@ -1,0 +1,211 @@
+"""GPU parity of the block attention kernel against the oracle.
+
+Bar: atol = rtol = 1e-2 against the float64 brute force (bf16 inputs, fp32
+softmax/accumulation in the kernel), on the same seeded inputs.
+
+Covers: the fp32 golden block-decode case (12/2 heads, 512 + 32 keys) run in
+bf16; the 7B-geometry bs16 paged sub-block decode at full size; the contiguous
+static-cache layout vs the paged layout (identical outputs); full 32-token
+blocks (224 rows per KV head); split-KV on/off; causal and block-causal masks;
+block-causal prefill with its KV-cache write; ragged lengths, empty sequences,
+a single visible key; fp16; head_dim 64.
+"""
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from fast_v2_amd import _ffi, ops, workloads
+from oracle import attention as oa
+
+pytestmark = pytest.mark.gpu
+
+ATOL = RTOL = 1e-2
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def _check(got: torch.Tensor, exp: np.ndarray, atol=ATOL, rtol=RTOL):
+    got = got.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, exp, atol=atol, rtol=rtol)
+
+
+def test_golden_small_decode_bf16(gpu):
+    """fp32 golden (torch CPU SDPA, 1 x 32 queries x 12/2 heads, 544 keys) vs the bf16 kernel."""
+    z = np.load(GOLDEN / "kv_decode_small.npz")
+    q = torch.from_numpy(z["q"]).to(torch.bfloat16)
+    k = torch.from_numpy(z["k"]).to(torch.bfloat16)
+    v = torch.from_numpy(z["v"]).to(torch.bfloat16)
+    seq = torch.from_numpy(z["seqlens"])
+    out = ops.block_attn(q.to(gpu), k.to(gpu), v.to(gpu), seq.to(gpu), float(z["scale"]))
+    # inputs were rounded to bf16: compare with both the bf16-input brute force (tight)
+    # and the fp32 golden output (loose, input rounding included)
+    _check(out, oa.attention_np(q.float(), k.float(), v.float(), seq, float(z["scale"])))
+    _check(out, z["out"], atol=3e-2, rtol=3e-2)
+
+
+@pytest.mark.parametrize("kv_split", [0, 64, 256, 1 << 20])
+def test_paged_subblock_decode_7b_bs16(gpu, kv_split):
+    wl = workloads.kv_decode_paged(seed=0)
+    print(f"case paged decode bs16 kv_split={kv_split} lens={wl.seqlens.tolist()}", flush=True)
+    out = ops.block_attn(wl.q.to(gpu), wl.k_pool.to(gpu), wl.v_pool.to(gpu), wl.seqlens.to(gpu), wl.scale,
+                         page_table=wl.page_table.to(gpu), page_size=wl.page_size,
+                         kv_split=min(kv_split, 1 << 16) if kv_split else 0)
+    exp = oa.attention_np(wl.q.float(), wl.k_pool.float(), wl.v_pool.float(), wl.seqlens, wl.scale,
+                          page_table=wl.page_table, page_size=wl.page_size)
+    _check(out, exp)
+
+
+def _paged_to_contig(wl, max_s):
+    B = wl.q.shape[0]
+    Hkv, D = wl.k_pool.shape[2], wl.k_pool.shape[3]
+    k = torch.zeros(B, max_s, Hkv, D, dtype=wl.k_pool.dtype)
+    v = torch.zeros_like(k)
+    for b in range(B):
+        L = int(wl.seqlens[b])
+        pos = torch.arange(L)
+        pages = wl.page_table[b, pos // wl.page_size].long()
+        k[b, :L] = wl.k_pool[pages, pos % wl.page_size]
+        v[b, :L] = wl.v_pool[pages, pos % wl.page_size]
+    return k, v
+
+
+def test_contiguous_equals_paged(gpu):
+    """The static BSHD cache [B, max_S, Hkv, D] (identity pages) gives bit-identical output."""
+    wl = workloads.kv_decode_paged(seed=1, batch=6, min_prefix=64, max_prefix=1024)
+    k, v = _paged_to_contig(wl, 1100)
+    a = ops.block_attn(wl.q.to(gpu), wl.k_pool.to(gpu), wl.v_pool.to(gpu), wl.seqlens.to(gpu), wl.scale,
+                       page_table=wl.page_table.to(gpu), page_size=wl.page_size)
+    b = ops.block_attn(wl.q.to(gpu), k.to(gpu), v.to(gpu), wl.seqlens.to(gpu), wl.scale)
+    assert torch.equal(a.cpu(), b.cpu())
+    # and the SDPA shim (the reference's CPU statement) agrees within tolerance
+    exp = oa.sdpa_kvcache(wl.q.float(), k.float(), v.float(), wl.seqlens, scaling=wl.scale)
+    _check(b, exp.numpy())
+
+
+@pytest.mark.parametrize("q_len", [1, 8, 32, 37])
+@pytest.mark.parametrize("mask_mode", [_ffi.MASK_SEQLEN, _ffi.MASK_CAUSAL, _ffi.MASK_BLOCK_CAUSAL])
+def test_masks_and_row_counts(gpu, q_len, mask_mode):
+    g = torch.Generator().manual_seed(q_len * 10 + mask_mode)
+    B, Hq, Hkv, D, max_s = 3, 28, 4, 128, 700
+    seqlens = torch.tensor([600, 37, 700], dtype=torch.int32)
+    q = torch.randn(B, q_len, Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, max_s, Hkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, max_s, Hkv, D, generator=g).to(torch.bfloat16)
+    print(f"case masks q_len={q_len} mode={mask_mode}", flush=True)
+    out = ops.block_attn(q.to(gpu), k.to(gpu), v.to(gpu), seqlens.to(gpu), None, mask_mode=mask_mode,
+                         mask_block=32, kv_split=128)
+    exp = oa.attention_np(q.float(), k.float(), v.float(), seqlens, None, mask_mode=mask_mode, mask_block=32)
+    _check(out, exp)
+
+
+def test_edge_lengths(gpu):
+    """Empty sequence -> zeros; one visible key -> that value row; keys past the length ignored."""
+    g = torch.Generator().manual_seed(7)
+    B, Sq, Hq, Hkv, D, S = 4, 8, 28, 4, 128, 300
+    q = torch.randn(B, Sq, Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, S, Hkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, S, Hkv, D, generator=g).to(torch.bfloat16)
+    seqlens = torch.tensor([0, 1, 65, 300], dtype=torch.int32)
+    # poison everything past each length with huge (finite) values
+    kp, vp = k.clone(), v.clone()
+    for b in range(B):
+        kp[b, int(seqlens[b]):] = 3e4
+        vp[b, int(seqlens[b]):] = -3e4
+    out = ops.block_attn(q.to(gpu), kp.to(gpu), vp.to(gpu), seqlens.to(gpu), kv_split=64).cpu()
+    assert torch.count_nonzero(out[0]) == 0
+    one_key = v[1, 0].float().repeat_interleave(Hq // Hkv, 0)[None].expand(Sq, Hq, D)
+    torch.testing.assert_close(out[1].float(), one_key, atol=0, rtol=0)
+    exp = oa.attention_np(q.float(), k.float(), v.float(), seqlens)
+    _check(out, exp)
+
+
+def test_fp16_and_head_dim_64(gpu):
+    g = torch.Generator().manual_seed(11)
+    for dtype, D, Hq, Hkv in ((torch.float16, 128, 28, 4), (torch.bfloat16, 64, 12, 2), (torch.float16, 64, 8, 8)):
+        B, Sq, S = 2, 32, 333
+        q = torch.randn(B, Sq, Hq, D, generator=g).to(dtype)
+        k = torch.randn(B, S, Hkv, D, generator=g).to(dtype)
+        v = torch.randn(B, S, Hkv, D, generator=g).to(dtype)
+        seqlens = torch.tensor([333, 200], dtype=torch.int32)
+        print(f"case {dtype} D={D} {Hq}/{Hkv}", flush=True)
+        out = ops.block_attn(q.to(gpu), k.to(gpu), v.to(gpu), seqlens.to(gpu), kv_split=128)
+        _check(out, oa.attention_np(q.float(), k.float(), v.float(), seqlens))
+
+
+def test_block_causal_prefill_with_cache_write(gpu):
+    """Block-causal prefill: write K/V into the static cache, attend with the block mask."""
+    wl = workloads.block_prefill(seed=0, batch=2, seq_len=512)
+    B, S, Hkv, D = wl.k.shape
+    kc = torch.zeros(B, 1024, Hkv, D, dtype=torch.bfloat16, device=gpu)
+    vc = torch.zeros_like(kc)
+    ops.kv_cache_write(wl.k.to(gpu), wl.v.to(gpu), kc, vc, write_offset=0)
+    assert torch.equal(kc[:, :S].cpu(), wl.k) and torch.count_nonzero(kc[:, S:]) == 0
+    seqlens = torch.full((B,), S, dtype=torch.int32, device=gpu)
+    out = ops.block_attn(wl.q.to(gpu), kc, vc, seqlens, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL,
+                         mask_block=wl.block)
+    exp = oa.sdpa_block_causal(wl.q.float(), wl.k.float(), wl.v.float(), wl.block)
+    _check(out, exp.numpy())
+
+
+def test_block_causal_prefill_full_size_sampled(gpu):
+    """4 x 4096 block-causal prefill; sampled query blocks checked against the brute force."""
+    wl = workloads.block_prefill(seed=0)
+    B, S, Hkv, D = wl.k.shape
+    kc = torch.empty(B, S, Hkv, D, dtype=torch.bfloat16, device=gpu)
+    vc = torch.empty_like(kc)
+    ops.kv_cache_write(wl.k.to(gpu), wl.v.to(gpu), kc, vc)
+    seqlens = torch.full((B,), S, dtype=torch.int32, device=gpu)
+    out = ops.block_attn(wl.q.to(gpu), kc, vc, seqlens, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL,
+                         mask_block=wl.block).cpu()
+    assert torch.equal(kc.cpu(), wl.k)
+    for blk in (0, 1, 63, 64, 127):
+        t0 = blk * wl.block
+        qs = torch.full((B,), t0, dtype=torch.int32)
+        exp = oa.attention_np(wl.q[:, t0:t0 + wl.block].float(), wl.k.float(), wl.v.float(),
+                              torch.full((B,), S), wl.scale, mask_mode=oa.MASK_BLOCK_CAUSAL,
+                              mask_block=wl.block, q_start=qs)
+        _check(out[:, t0:t0 + wl.block], exp)
+
+
+def test_flash_kvcache_op_and_meta(gpu):
+    wl = workloads.kv_decode_paged(seed=2, batch=2, min_prefix=64, max_prefix=256)
+    k, v = _paged_to_contig(wl, 320)
+    out = torch.ops.fdllm.flash_kvcache(wl.q.to(gpu), k.to(gpu), v.to(gpu), wl.seqlens.to(gpu), wl.scale, False)
+    _check(out, oa.attention_np(wl.q.float(), k.float(), v.float(), wl.seqlens, wl.scale))
+    meta = torch.ops.fdllm.flash_kvcache(wl.q.to("meta"), k.to("meta"), v.to("meta"),
+                                         wl.seqlens.to("meta"), wl.scale, False)
+    assert meta.shape == wl.q.shape and meta.device.type == "meta"
+
+
+def test_repeated_split_calls_rearm(gpu):
+    """Split-KV completion counters are re-armed: many calls in a row stay correct."""
+    wl = workloads.kv_decode_paged(seed=3, batch=4, min_prefix=512, max_prefix=2048)
+    q, kp, vp = wl.q.to(gpu), wl.k_pool.to(gpu), wl.v_pool.to(gpu)
+    pt, sl = wl.page_table.to(gpu), wl.seqlens.to(gpu)
+    first = ops.block_attn(q, kp, vp, sl, wl.scale, page_table=pt, page_size=wl.page_size, kv_split=128)
+    for _ in range(20):
+        again = ops.block_attn(q, kp, vp, sl, wl.scale, page_table=pt, page_size=wl.page_size, kv_split=128)
+    assert torch.equal(first, again)
+
+
+def test_workspace_reuse_across_shapes(gpu):
+    """One workspace serves consecutive split calls of different sizes: a small call
+    (few work units) followed by a large one (many units) must not read the small
+    call's partials as completion counters."""
+    small = workloads.kv_decode_paged(seed=4, batch=2, min_prefix=512, max_prefix=1024)
+    ops.block_attn(small.q.to(gpu), small.k_pool.to(gpu), small.v_pool.to(gpu), small.seqlens.to(gpu),
+                   small.scale, page_table=small.page_table.to(gpu), page_size=small.page_size, kv_split=64)
+    wl = workloads.block_prefill(seed=0, batch=2, seq_len=512)
+    B, S, Hkv, D = wl.k.shape
+    kc = torch.zeros(B, 1024, Hkv, D, dtype=torch.bfloat16, device=gpu)
+    vc = torch.zeros_like(kc)
+    kc[:, :S] = wl.k.to(gpu)
+    vc[:, :S] = wl.v.to(gpu)
+    sl = torch.full((B,), S, dtype=torch.int32, device=gpu)
+    exp = oa.sdpa_block_causal(wl.q.float(), wl.k.float(), wl.v.float(), wl.block).numpy()
+    for split in (64, 256, 0):
+        out = ops.block_attn(wl.q.to(gpu), kc, vc, sl, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL,
+                             mask_block=wl.block, kv_split=split)
+        _check(out, exp)
