@@ -1,0 +1,379 @@
+#!/usr/bin/env python3
+"""Benchmark of the block-diffusion hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline] [--only NAME]
+
+Headline (one JSON line on stdout): the block-decode attention step at 7B
+geometry — 16 sequences, 28 query / 4 KV heads, head_dim 128, prefixes uniform
+in {1024..4096} step 32 plus the current 32-token block, 8 active queries (one
+sub-block), 32-token KV pages, bf16. One step = one attention call of one layer;
+the K timed steps walk through 28 separate layer pools (2.4 GB of KV), so every
+call streams its KV from HBM rather than from the 256 MB last-level cache.
+
+The K steps are captured in one HIP graph and replayed once inside the timed
+region, bracketed by torch.cuda.synchronize(); HIP events recorded on the same
+stream give the per-step time, i.e. the average kernel duration plus the
+inter-kernel gap.
+
+Also reported (same run, under "extra"): gather + RMSNorm (bf16 [4096 x 3584],
+1024 rows) and block-causal prefill with its KV-cache write (4 x 4096 tokens),
+each with its own roofline.
+
+cpu_baseline: the reference's CPU path for the same workload, the SDPA shim of
+tests/test_focus.py:205-228 (oracle.attention.sdpa_kvcache), on the host cores.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_BF16_PEAK_TFLOPS = 2500.0  # MI355X dense bf16 MFMA, TFLOP/s
+METRIC = "block-attn step µs + % HBM/MFMA peak; gen tokens/s (7B geom, bs16)"
+LAYERS = 28
+TRAFFIC_FILE = ROOT / "profiles" / "traffic.json"
+
+
+def _log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def _time_graph(torch, step_fn, steps: int, warmup: int) -> float:
+    """Run `warmup` eager steps, capture `steps` steps in one graph, replay it once
+    untimed, then time one replay. Returns microseconds per step.
+
+    Warm-up runs on the capture stream so that any per-stream scratch the ops keep
+    (the split-KV workspace) exists before capture starts."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for i in range(warmup):
+            step_fn(i)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for i in range(steps):
+            step_fn(i)
+    torch.cuda.synchronize()
+    g.replay()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    g.replay()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / steps
+    del g
+    return us
+
+
+def _traffic(name: str):
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+        return data.get(name)
+    except (OSError, ValueError):
+        return None
+
+
+def _roofline(bound: str, achieved: float, peak: float, unit: str, traffic):
+    return {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+            "frac": round(achieved / peak, 4), "traffic": traffic}
+
+
+# ---------------------------------------------------------------------------
+def bench_decode(torch, args):
+    from fast_v2_amd import ops, workloads
+
+    dev = torch.device("cuda", 0)
+    wl = workloads.kv_decode_paged(seed=0)
+    layers = args.layers
+    # layer 0 holds the seeded pool (shared with the CPU baseline); further layers are
+    # N(0,1) pools drawn on the device, same page table
+    gen = torch.Generator(device=dev).manual_seed(1)
+    kp = torch.empty((layers,) + tuple(wl.k_pool.shape), dtype=wl.k_pool.dtype, device=dev)
+    vp = torch.empty_like(kp)
+    kp[0].copy_(wl.k_pool)
+    vp[0].copy_(wl.v_pool)
+    for layer in range(1, layers):
+        kp[layer].normal_(generator=gen)
+        vp[layer].normal_(generator=gen)
+    q = wl.q.to(dev)
+    pt = wl.page_table.to(dev)
+    sl = wl.seqlens.to(dev)
+    page_size = wl.page_size
+    if args.layout == "contig":
+        # the reference's static cache layout [B, max_S, Hkv, D] per layer (identity pages)
+        B = q.shape[0]
+        max_s = int(wl.seqlens.max())
+        pos = torch.arange(max_s, device=dev)
+        idx = pt[:, (pos // page_size).clamp(max=pt.shape[1] - 1)].long()  # [B, max_S]
+        kc = kp[:, idx, pos % page_size]  # [layers, B, max_S, Hkv, D]
+        vc = vp[:, idx, pos % page_size]
+        kp, vp, pt, page_size = kc, vc, None, 0
+        torch.cuda.empty_cache()
+    _log(f"decode: lens={wl.seqlens.tolist()} layout={args.layout} "
+         f"kv={2 * kp.numel() * 2 / 2**30:.2f} GiB over {layers} layers")
+    out = torch.empty_like(q)
+    B, Sq, Hq, D = q.shape
+    Hkv = kp.shape[-2]
+
+    def step(i):
+        layer = i % layers
+        ops.block_attn(q, kp[layer], vp[layer], sl, wl.scale, page_table=pt, page_size=page_size,
+                       out=out, kv_split=args.kv_split)
+
+    # graph replay must reproduce the eager result bit for bit
+    step(layers - 1)
+    eager = out.clone()
+    us = _time_graph(torch, step, args.steps, args.warmup)
+    if args.steps % layers == 0 and not args.no_check and not torch.equal(out, eager):
+        raise RuntimeError("graph replay output differs from the eager call")
+    nbytes = workloads.decode_bytes(wl.seqlens, Hq, Hkv, D, Sq)
+    flops = workloads.decode_flops(wl.seqlens, Hq, D, Sq)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    res = {
+        "us_per_step": us,
+        "bytes_per_step": nbytes,
+        "flops_per_step": flops,
+        "achieved_gbs": gbs,
+        "tflops": flops / (us * 1e-6) / 1e12,
+        "roofline": _roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s", _traffic("kv_attn_decode_bs16")),
+        "us_per_model_step_28_layers": us * LAYERS,
+        "seqlens": wl.seqlens.tolist(),
+    }
+    del q, kp, vp, pt, sl, out
+    torch.cuda.empty_cache()
+    return res, wl
+
+
+def cpu_baseline_decode(torch, wl, seconds: float):
+    """Reference CPU path (SDPA shim) on the same bs16 inputs, bf16, contiguous static cache."""
+    from oracle import attention as oa
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    B, Sq, Hq, D = wl.q.shape
+    Hkv = wl.k_pool.shape[-2]
+    max_s = int(wl.seqlens.max())
+    layer_k, layer_v = wl.k_pool, wl.v_pool
+    k = torch.zeros(B, max_s, Hkv, D, dtype=wl.q.dtype)
+    v = torch.zeros_like(k)
+    for b in range(B):
+        L = int(wl.seqlens[b])
+        pos = torch.arange(L)
+        pages = wl.page_table[b, pos // wl.page_size].long()
+        k[b, :L] = layer_k[pages, pos % wl.page_size]
+        v[b, :L] = layer_v[pages, pos % wl.page_size]
+    oa.sdpa_kvcache(wl.q, k, v, wl.seqlens, scaling=wl.scale)  # warm
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        oa.sdpa_kvcache(wl.q, k, v, wl.seqlens, scaling=wl.scale)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times) * 1e6
+    return {"value": round(med, 1), "unit": "us/step", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"SDPA shim (tests/test_focus.py:205-228 restated in oracle/attention.py), bf16, "
+                       f"the full bs16 batch of one layer, contiguous [16, {max_s}, 4, 128] cache; "
+                       f"median of {len(times)} calls over ~{seconds:.0f} s")}
+
+
+# ---------------------------------------------------------------------------
+def bench_gather(torch, args):
+    from fast_v2_amd import _ffi, ops, workloads
+
+    dev = torch.device("cuda", 0)
+    wl = workloads.gather_rmsnorm_rows(seed=0)
+    copies = 16  # 16 x 29 MB of hidden states: larger than the last-level cache
+    hs = [wl.hidden.to(dev)]
+    for _ in range(copies - 1):
+        hs.append(hs[0].clone())
+    idx = wl.indices.to(dev)
+    w = wl.weight.to(dev)
+    res = {}
+    for name, with_g in (("normed", False), ("pair", True)):
+        def step(i, with_g=with_g):
+            ops.gather_rmsnorm(hs[i % copies], idx, w, wl.eps, _ffi.NORM_WEIGHT_AFTER_CAST, with_g)
+        steps = args.gather_steps
+        us = _time_graph(torch, step, steps, min(args.warmup, 32))
+        T, H = idx.shape[1], wl.hidden.shape[2]
+        nbytes = workloads.gather_bytes(T, H, 2, with_gathered=with_g)
+        gbs = nbytes / (us * 1e-6) / 1e9
+        res[name] = {"us_per_call": us, "bytes_per_call": nbytes, "achieved_gbs": gbs,
+                     "roofline": _roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s",
+                                           _traffic(f"gather_rmsnorm_{name}"))}
+    del hs
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_prefill(torch, args):
+    from fast_v2_amd import _ffi, ops, workloads
+
+    dev = torch.device("cuda", 0)
+    wl = workloads.block_prefill(seed=0)
+    q, k, v = wl.q.to(dev), wl.k.to(dev), wl.v.to(dev)
+    B, S, Hq, D = q.shape
+    Hkv = k.shape[2]
+    kc = torch.zeros(B, S, Hkv, D, dtype=q.dtype, device=dev)
+    vc = torch.zeros_like(kc)
+    sl = torch.full((B,), S, dtype=torch.int32, device=dev)
+    out = torch.empty_like(q)
+
+    def attn_only(i):
+        ops.block_attn(q, kc, vc, sl, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL, mask_block=wl.block, out=out)
+
+    def full(i):
+        ops.kv_cache_write(k, v, kc, vc, write_offset=0)
+        attn_only(i)
+
+    steps = args.prefill_steps
+    us_full = _time_graph(torch, full, steps, 2)
+    us_attn = _time_graph(torch, attn_only, steps, 2)
+    flops = workloads.prefill_flops(B, S, Hq, D, wl.block)
+    nbytes = workloads.prefill_bytes(B, S, Hq, Hkv, D)
+    tf = flops / (us_attn * 1e-6) / 1e12
+    res = {"us_per_call_with_cache_write": us_full, "us_attention_kernel": us_attn,
+           "flops": flops, "bytes_with_cache_write": nbytes,
+           "roofline": _roofline("mfma", tf, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", _traffic("kv_attn_prefill")),
+           "tflops_with_cache_write": flops / (us_full * 1e-6) / 1e12}
+    del q, k, v, kc, vc, out
+    torch.cuda.empty_cache()
+    return res
+
+
+def calibrate_copies(torch):
+    """Plain torch device copies (read N + write N bytes) timed the same way as the
+    kernels: the practical bandwidth of a kernel of that size, launch gap included."""
+    res = {}
+    for mb in (7, 48, 256, 1024):
+        n = mb << 20
+        bufs = [torch.empty(n, dtype=torch.uint8, device="cuda") for _ in range(4 if mb < 256 else 2)]
+        dsts = [torch.empty(n, dtype=torch.uint8, device="cuda") for _ in bufs]
+
+        def step(i):
+            dsts[i % len(bufs)].copy_(bufs[i % len(bufs)])
+        steps = 200 if mb < 256 else 20
+        us = _time_graph(torch, step, steps, 4)
+        res[f"copy_{mb}MiB"] = {"us": round(us, 2), "GBs_read_plus_write": round(2 * n / (us * 1e-6) / 1e9, 1)}
+        del bufs, dsts
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1120, help="timed attention steps (multiple of 28 keeps layers balanced)")
+    ap.add_argument("--warmup", type=int, default=56)
+    ap.add_argument("--gather-steps", type=int, default=2000)
+    ap.add_argument("--prefill-steps", type=int, default=20)
+    ap.add_argument("--kv-split", type=int, default=0, help="keys per split-KV work item (0 = automatic)")
+    ap.add_argument("--layers", type=int, default=LAYERS, help="layer pools cycled by the decode steps")
+    ap.add_argument("--layout", choices=["paged", "contig"], default="paged",
+                    help="KV layout: 32-token pages, or the contiguous [B, max_S, Hkv, D] static cache")
+    ap.add_argument("--no-check", action="store_true", help="skip the graph-vs-eager equality check")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", choices=["decode", "gather", "prefill"], default=None)
+    ap.add_argument("--calibrate", action="store_true",
+                    help="also time plain device copies of the workloads' sizes (practical bandwidth floor)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first run a plain 512 MiB device copy (for HBM counter calibration)")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build targets one GPU: the block-decode attention and gather+RMSNorm "
+                          "kernels run on one GPU's share; multi-GPU runs are not part of it",
+                          "n_gpus": args.gpus}), flush=True)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}), flush=True)
+        return 1
+    from fast_v2_amd import _ffi
+    _ffi.lib()  # fail loudly if the HIP library is missing
+
+    if args.copy_calibration:
+        src = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
+
+    calib = None
+    if args.calibrate:
+        calib = calibrate_copies(torch)
+        _log(f"calibration: {json.dumps(calib)}")
+
+    extra = {}
+    decode = wl = None
+    if args.only in (None, "decode"):
+        decode, wl = bench_decode(torch, args)
+        _log(f"decode: {decode['us_per_step']:.2f} us/step, {decode['achieved_gbs']:.0f} GB/s")
+    if args.only in (None, "gather"):
+        extra["gather_rmsnorm"] = bench_gather(torch, args)
+        _log(f"gather: {json.dumps({k: round(v['us_per_call'], 3) for k, v in extra['gather_rmsnorm'].items()})} us")
+    if args.only in (None, "prefill"):
+        extra["prefill"] = bench_prefill(torch, args)
+        _log(f"prefill: {extra['prefill']['us_attention_kernel']:.1f} us attention, "
+             f"{extra['prefill']['roofline']['achieved']:.0f} TFLOP/s")
+
+    cpu = None
+    if decode is not None and not args.no_cpu_baseline:
+        _log("cpu baseline ...")
+        cpu = cpu_baseline_decode(torch, wl, args.cpu_seconds)
+
+    if decode is not None:
+        us = decode["us_per_step"]
+        line = {
+            "metric": METRIC,
+            "value": round(us, 3),
+            "unit": "us/step",
+            "n_gpus": 1,
+            "steps": args.steps,
+            "warmup": args.warmup,
+            "ms_per_step": round(us / 1e3, 6),
+            "higher_is_better": False,
+            "scaling": "weak",
+            "vs_baseline": None,
+            "dtype": "bf16",
+            "data": "synthetic",
+            "config": {
+                "workload": ("block-decode attention, 7B geometry: batch 16, 28 query / 4 KV heads, head_dim 128, "
+                             "prefix U{1024..4096 step 32} + 32-token block, 8 active queries, 32-token pages, "
+                             "one layer per step over 28 layer pools"),
+                "batch": 16, "q_len": 8, "num_q_heads": 28, "num_kv_heads": 4, "head_dim": 128,
+                "page_size": 32, "layers_cycled": LAYERS, "seqlens": decode["seqlens"],
+            },
+            "roofline": decode["roofline"],
+            "cpu_baseline": cpu,
+            "extra": {
+                "decode": {k: decode[k] for k in ("bytes_per_step", "flops_per_step", "tflops",
+                                                  "us_per_model_step_28_layers")},
+                **extra,
+            },
+        }
+    else:
+        line = {"metric": METRIC, "value": None, "extra": extra}
+    if calib is not None:
+        line.setdefault("extra", {})["copy_calibration"] = calib
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

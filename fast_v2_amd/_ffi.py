@@ -15,7 +15,10 @@ from pathlib import Path
 
 import torch  # noqa: F401  (must precede the library load, see above)
 
-LIB_PATH = Path(__file__).resolve().parent / "lib" / "libfdllm_hip.so"
+import os
+
+# FDLLM_HIP_LIB overrides the location of the library (default: the in-tree build).
+LIB_PATH = Path(os.environ.get("FDLLM_HIP_LIB") or (Path(__file__).resolve().parent / "lib" / "libfdllm_hip.so"))
 
 FDLLM_OK = 0
 FDLLM_ERR_INVALID_ARGUMENT = -1

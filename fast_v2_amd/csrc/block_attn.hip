@@ -14,11 +14,13 @@
 //     16-row M-tiles, so a workgroup covers 64 * MT rows and every K/V byte
 //     fetched from HBM serves all G heads of the group.
 //   * Keys. Each workgroup streams one split of the sequence's keys in tiles of
-//     64. A tile is loaded with coalesced 16-byte global loads into registers
-//     one iteration ahead (double buffering through registers), then written
-//     to LDS: K row-major with a 16-byte row pad, V transposed ([d][key]) with
-//     an 8-byte row pad, so that both MFMA operands are read as contiguous
-//     LDS vectors without bank conflicts.
+//     64. Tiles are fetched two ahead into registers with coalesced 16-byte
+//     loads (page ids one step further ahead, issued before the tile loads so
+//     the in-order vmcnt counter never drains the prefetch), then written to
+//     LDS: K row-major with a 16-byte row pad, V transposed ([d][key]) with an
+//     8-byte row pad, so both MFMA operands are read as contiguous LDS vectors
+//     without bank conflicts. Workgroup barriers fence LDS only, so global
+//     loads stay in flight across them.
 //   * Math. S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (keys along M, query rows
 //     along N, so each lane owns one query row), online softmax in the base-2
 //     domain with a 4-lane-group max reduction, then O^T = V^T P^T with the
@@ -28,9 +30,10 @@
 //   * Masks are arithmetic: key < row limit, where the limit per row comes from
 //     seqlens / q_start / mask_block. Keys past the limit are never loaded.
 //   * Split-KV. When one (sequence, KV head) is split over several workgroups,
-//     each writes an unnormalised partial (O, m, l) to the workspace, and the
-//     last workgroup to finish (device-scope counter) merges them and writes
-//     the output, then re-arms the counter. No second kernel launch.
+//     each writes an unnormalised partial (O, m, l) to the workspace and a
+//     second, fully parallel kernel merges them (16 threads per row, all
+//     splits' loads in flight). The kernel boundary orders the two, so no
+//     device-scope fence or counter is needed.
 #include <algorithm>
 
 #include "fdllm_common.h"
@@ -53,7 +56,7 @@ struct AttnParams {
   const int32_t* page_table;
   const int32_t* seqlens;
   const int32_t* q_start;
-  int max_pages, page_size, max_seqlen;
+  int max_pages, page_size, page_shift, max_seqlen;  // page_size == 1 << page_shift
   int B, Sq, Hq, Hkv, G;
   int R;            // rows per (b, kv head) = Sq * G
   int rows_per_wg;  // 64 * MT
@@ -64,7 +67,6 @@ struct AttnParams {
   float scale_log2;  // softmax_scale * log2(e)
   float* ws_o;       // [units, n_splits, rows_per_wg, D]
   float2* ws_ml;     // [units, n_splits, rows_per_wg]
-  int* ws_cnt;       // [units]
 };
 
 template <bool F16>
@@ -87,6 +89,14 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   }
 }
 
+// Workgroup barrier that orders LDS only: waits for this wave's LDS operations,
+// then s_barrier. Outstanding global loads stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Exclusive key bound for query token t of sequence b.
 __device__ __forceinline__ int row_key_limit(const AttnParams& p, int seqlen, int qs, int t) {
   if (p.mask_mode == FDLLM_MASK_SEQLEN) return seqlen;
@@ -100,16 +110,31 @@ __device__ __forceinline__ int row_key_limit(const AttnParams& p, int seqlen, in
   return lim < seqlen ? lim : seqlen;
 }
 
-// Pointer to row (key j, kv head h) of the K or V pool for sequence b.
-__device__ __forceinline__ int64_t kv_offset(const AttnParams& p, int b, int j, int64_t sp, int64_t ss) {
-  if (p.page_table) {
-    const int page = p.page_table[static_cast<int64_t>(b) * p.max_pages + j / p.page_size];
-    return page * sp + (j % p.page_size) * ss;
-  }
-  return b * sp + j * ss;
+// Per (sequence, row block) facts shared by the attention and combine kernels.
+struct SeqInfo {
+  int seqlen;  // visible KV length after clamping to the cache capacity
+  int qs;      // absolute position of query token 0
+  int kv_end;  // keys any row of the row block may see
+  int n_act;   // splits that hold at least one of those keys
+};
+
+template <bool PAGED>
+__device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b, int rb) {
+  SeqInfo si;
+  int seqlen = p.seqlens[b];
+  if (seqlen > p.max_seqlen) seqlen = p.max_seqlen;
+  if (PAGED && seqlen > p.max_pages * p.page_size) seqlen = p.max_pages * p.page_size;
+  if (seqlen < 0) seqlen = 0;
+  si.seqlen = seqlen;
+  si.qs = p.q_start ? p.q_start[b] : seqlen - p.Sq;
+  const int row0 = rb * p.rows_per_wg;
+  const int row_last = min(p.R, row0 + p.rows_per_wg) - 1;  // limits grow with t
+  si.kv_end = max(0, row_key_limit(p, seqlen, si.qs, row_last / p.G));
+  si.n_act = (si.kv_end + p.chunk - 1) / p.chunk;
+  return si;
 }
 
-template <int D, int MT, bool F16>
+template <int D, int MT, bool F16, bool PAGED>
 __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
   constexpr int KS = D + 8;      // K row stride in LDS (elements), 16-byte pad
   constexpr int VS = kKT + 4;    // V^T row stride in LDS (elements), 8-byte pad
@@ -120,7 +145,6 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
   static_assert(KLD >= 1, "tile too small");
   __shared__ __attribute__((aligned(16))) uint16_t sK[kKT * KS];
   __shared__ __attribute__((aligned(16))) uint16_t sVt[D * VS];
-  __shared__ int s_is_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -135,41 +159,26 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
   const int kvh = bh - b * p.Hkv;
   const int unit = bh * p.n_rb + rb;
 
-  int seqlen = p.seqlens[b];
-  if (seqlen > p.max_seqlen) seqlen = p.max_seqlen;
-  if (p.page_table && seqlen > p.max_pages * p.page_size) seqlen = p.max_pages * p.page_size;
-  if (seqlen < 0) seqlen = 0;
-  const int qs = p.q_start ? p.q_start[b] : seqlen - p.Sq;
-
-  // Key range of this workgroup: up to the limit of its last valid row.
+  const SeqInfo si = seq_info<PAGED>(p, b, rb);
+  if (split >= max(si.n_act, 1)) return;
   const int row0 = rb * p.rows_per_wg;
-  const int row_last = min(p.R, row0 + p.rows_per_wg) - 1;
-  const int kv_end = max(0, row_key_limit(p, seqlen, qs, row_last / p.G));
-  const int n_act = (kv_end + p.chunk - 1) / p.chunk;
-  if (split >= max(n_act, 1)) return;
   const int k_lo = split * p.chunk;
-  const int k_hi = min(kv_end, k_lo + p.chunk);
+  const int k_hi = min(si.kv_end, k_lo + p.chunk);
+  const int ntiles = k_hi > k_lo ? (k_hi - k_lo + kKT - 1) / kKT : 0;
 
   // ---- per-lane query rows, Q fragments (B operand of S^T = K Q^T), row limits
   u32x4 qf[MT][NKS];
   int lim[MT];
-  bool mt_valid[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int r = row0 + (wave * MT + mt) * 16 + l16;
-    mt_valid[mt] = (row0 + (wave * MT + mt) * 16) < p.R;
-    if (r < p.R) {
-      const int t = r / p.G;
-      const int hh = r - t * p.G;
-      lim[mt] = row_key_limit(p, seqlen, qs, t);
-      const uint16_t* qrow = p.q + b * p.q_sb + t * p.q_ss + (kvh * p.G + hh) * p.q_sh;
+    const int rc = min(r, p.R - 1);  // padding rows read a valid row; their limit is 0
+    const int t = rc / p.G;
+    const int hh = rc - t * p.G;
+    lim[mt] = r < p.R ? row_key_limit(p, si.seqlen, si.qs, t) : 0;
+    const uint16_t* qrow = p.q + b * p.q_sb + t * p.q_ss + (kvh * p.G + hh) * p.q_sh;
 #pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) qf[mt][ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 32 + g * 8);
-    } else {
-      lim[mt] = 0;
-#pragma unroll
-      for (int ks = 0; ks < NKS; ++ks) qf[mt][ks] = u32x4{0u, 0u, 0u, 0u};
-    }
+    for (int ks = 0; ks < NKS; ++ks) qf[mt][ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 32 + g * 8);
   }
 
   f32x4 acc[MT][NDT];
@@ -182,42 +191,72 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
     for (int dt = 0; dt < NDT; ++dt) acc[mt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
 
-  // ---- global -> register staging of one 64-key tile
-  u32x4 kreg[KLD];
-  u32x4 vreg[4];
-  const int v_kq = tid & 15;   // key quad
-  const int v_dq = tid >> 4;   // d octet
-  const bool v_active = v_dq < KCH;
-  auto load_tile = [&](int kb) {
+  // ---- global -> register staging. Loads are unconditional: keys at or past
+  // k_hi are clamped to k_hi - 1, a valid key whose score is masked to -inf
+  // (p = 0 against finite data), so no branch separates a tile's loads.
+  constexpr bool kVAll = (kThreads / 16) == KCH;  // every thread stages V (D == 128)
+  const int v_kq = tid & 15;  // key quad
+  const int v_dq = tid >> 4;  // d octet
+  const bool v_active = kVAll || v_dq < KCH;
+  const int32_t* pt_row = PAGED ? p.page_table + static_cast<int64_t>(b) * p.max_pages : nullptr;
+
+  struct Stage {
+    u32x4 k[KLD];
+    u32x4 v[4];
+  };
+  // Pages of the keys this thread stages for one tile (paged pools). Page sizes
+  // are powers of two >= 16, so each aligned 16-key group of K lives in one page
+  // (the same for the whole workgroup: scalar loads) and each aligned 4-key group
+  // of V in one page (one id per lane). Clamping stays inside the group.
+  struct Rows {
+    int kpg[KLD];
+    int vpg;
+  };
+  Stage st0;
+  Stage st1;  // unused (and removed by the compiler) when kDepth == 1
+  Rows rs0, rs1;  // unused without a page table
+
+  auto kkey = [&](int kb, int i) { return min(kb + (tid + kThreads * i) / KCH, k_hi - 1); };
+  auto vkey = [&](int kb, int r) { return min(kb + v_kq * 4 + r, k_hi - 1); };
+  auto resolve = [&](Rows& rs, int kb) {
+    if constexpr (PAGED) {
+#pragma unroll
+      for (int i = 0; i < KLD; ++i) {
+        // keys kb + i * (kThreads / KCH) + tid / KCH: one aligned group of kThreads / KCH
+        // keys per i (16 for D == 128, 32 for D == 64); the host requires
+        // page_size >= kThreads / KCH so the group sits in one page
+        const int k0 = min(kb + i * (kThreads / KCH), k_hi - 1);
+        rs.kpg[i] = pt_row[k0 >> p.page_shift];
+      }
+      rs.vpg = pt_row[min(kb + v_kq * 4, k_hi - 1) >> p.page_shift];
+    }
+  };
+  auto row_off = [&](int key, int page, int64_t sp, int64_t ss) -> int64_t {
+    if constexpr (PAGED) {
+      return static_cast<int64_t>(page) * sp + (key & (p.page_size - 1)) * ss;
+    } else {
+      return b * sp + key * ss;
+    }
+  };
+  auto load_tile = [&](Stage& st, const Rows& rs, int kb) {
 #pragma unroll
     for (int i = 0; i < KLD; ++i) {
-      const int c = tid + kThreads * i;
-      const int key = kb + c / KCH;
-      const int dc = c % KCH;
-      if (key < k_hi) {
-        kreg[i] = *reinterpret_cast<const u32x4*>(p.k + kv_offset(p, b, key, p.k_sp, p.k_ss) + kvh * p.k_sh + dc * 8);
-      } else {
-        kreg[i] = u32x4{0u, 0u, 0u, 0u};
-      }
+      const int dc = (tid + kThreads * i) % KCH;
+      st.k[i] = *reinterpret_cast<const u32x4*>(p.k + row_off(kkey(kb, i), rs.kpg[i], p.k_sp, p.k_ss) +
+                                                kvh * p.k_sh + dc * 8);
     }
     if (v_active) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kb + v_kq * 4 + r;
-        if (key < k_hi) {
-          vreg[r] =
-              *reinterpret_cast<const u32x4*>(p.v + kv_offset(p, b, key, p.v_sp, p.v_ss) + kvh * p.v_sh + v_dq * 8);
-        } else {
-          vreg[r] = u32x4{0u, 0u, 0u, 0u};
-        }
-      }
+      for (int r = 0; r < 4; ++r)
+        st.v[r] = *reinterpret_cast<const u32x4*>(p.v + row_off(vkey(kb, r), rs.vpg, p.v_sp, p.v_ss) +
+                                                  kvh * p.v_sh + v_dq * 8);
     }
   };
-  auto store_tile = [&]() {
+  auto store_tile = [&](const Stage& st) {
 #pragma unroll
     for (int i = 0; i < KLD; ++i) {
       const int c = tid + kThreads * i;
-      *reinterpret_cast<u32x4*>(&sK[(c / KCH) * KS + (c % KCH) * 8]) = kreg[i];
+      *reinterpret_cast<u32x4*>(&sK[(c / KCH) * KS + (c % KCH) * 8]) = st.k[i];
     }
     if (v_active) {
       // 4 keys x 8 d  ->  8 rows of V^T, 4 consecutive keys each (8 bytes)
@@ -226,25 +265,19 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
         const int w = e >> 1;
         uint32_t lo, hi;
         if (e & 1) {
-          lo = (vreg[0][w] >> 16) | (vreg[1][w] & 0xffff0000u);
-          hi = (vreg[2][w] >> 16) | (vreg[3][w] & 0xffff0000u);
+          lo = (st.v[0][w] >> 16) | (st.v[1][w] & 0xffff0000u);
+          hi = (st.v[2][w] >> 16) | (st.v[3][w] & 0xffff0000u);
         } else {
-          lo = (vreg[0][w] & 0xffffu) | (vreg[1][w] << 16);
-          hi = (vreg[2][w] & 0xffffu) | (vreg[3][w] << 16);
+          lo = (st.v[0][w] & 0xffffu) | (st.v[1][w] << 16);
+          hi = (st.v[2][w] & 0xffffu) | (st.v[3][w] << 16);
         }
         *reinterpret_cast<u32x2*>(&sVt[(v_dq * 8 + e) * VS + v_kq * 4]) = u32x2{lo, hi};
       }
     }
   };
 
-  if (k_lo < k_hi) load_tile(k_lo);
-  for (int kb = k_lo; kb < k_hi; kb += kKT) {
-    __syncthreads();  // previous tile fully consumed
-    store_tile();
-    __syncthreads();
-    if (kb + kKT < k_hi) load_tile(kb + kKT);
-
-    // ---- S^T = K Q^T for four 16-key sub-tiles
+  // ---- one 64-key tile from LDS: S^T = K Q^T, online softmax, O^T += V^T P^T
+  auto compute_tile = [&](int kb) {
     f32x4 s[MT][4];
 #pragma unroll
     for (int st = 0; st < 4; ++st) {
@@ -255,15 +288,12 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
         f32x4 c = {0.f, 0.f, 0.f, 0.f};
-        if (mt_valid[mt]) {
 #pragma unroll
-          for (int ks = 0; ks < NKS; ++ks) c = mfma16x16x32<F16>(kf[ks], qf[mt][ks], c);
-        }
+        for (int ks = 0; ks < NKS; ++ks) c = mfma16x16x32<F16>(kf[ks], qf[mt][ks], c);
         s[mt][st] = c;
       }
     }
-
-    // ---- online softmax (base 2); lane owns query row l16 of each M-tile
+    // lane owns query row l16 of each M-tile; its 16 scores sit at keys kb + 16st + 4g + j
     u32x4 pf[MT][2];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -306,8 +336,6 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
         pf[mt][kk][3] = pack2<F16>(s[mt][2 * kk + 1][2], s[mt][2 * kk + 1][3]);
       }
     }
-
-    // ---- O^T += V^T P^T
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
@@ -317,9 +345,51 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
         const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 16);
         const u32x4 vf = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          if (mt_valid[mt]) acc[mt][dt] = mfma16x16x32<F16>(vf, pf[mt][kk], acc[mt][dt]);
-        }
+        for (int mt = 0; mt < MT; ++mt) acc[mt][dt] = mfma16x16x32<F16>(vf, pf[mt][kk], acc[mt][dt]);
+      }
+    }
+  };
+
+  // Prefetch depth: decode-shaped workgroups (MT <= 2) keep two tiles in flight;
+  // MT == 4 (prefill) has 4x the math per tile, which hides a one-tile prefetch,
+  // and not the registers for a second stage.
+  constexpr int kDepth = MT <= 2 ? 2 : 1;
+  // At step t the page ids of tile t + kDepth + 1 are requested first, then the
+  // loads of tile t + kDepth, so waiting for the page ids one step later never
+  // waits for those tile loads (vmcnt retires in issue order). Every step issues
+  // the same loads whether or not the tiles exist (keys clamp to k_hi - 1, so
+  // surplus loads re-read one cached row): the number of loads in flight is the
+  // same on every path, which lets the compiler wait for exactly the stage it
+  // needs instead of draining the prefetch. Only the LDS math is conditional.
+  auto step = [&](Stage& st, Rows& rs_load, Rows& rs_resolve, int t) {
+    lds_barrier();  // every wave is done reading the previous tile
+    store_tile(st);
+    lds_barrier();
+    resolve(rs_resolve, k_lo + (t + kDepth + 1) * kKT);
+    load_tile(st, rs_load, k_lo + (t + kDepth) * kKT);
+    if (t < ntiles) compute_tile(k_lo + t * kKT);
+  };
+
+  if (ntiles > 0) {
+    if constexpr (kDepth == 2) {
+      // tile t in stage t % 2; pages of tile t + 2 in rs[t % 2]
+      resolve(rs0, k_lo);
+      resolve(rs1, k_lo + kKT);
+      load_tile(st0, rs0, k_lo);
+      load_tile(st1, rs1, k_lo + kKT);
+      resolve(rs0, k_lo + 2 * kKT);
+      for (int t = 0; t < ntiles; t += 2) {
+        step(st0, rs0, rs1, t);
+        step(st1, rs1, rs0, t + 1);
+      }
+    } else {
+      // one stage; pages of tile t + 1 in rs[(t + 1) % 2]
+      resolve(rs0, k_lo);
+      load_tile(st0, rs0, k_lo);
+      resolve(rs1, k_lo + kKT);
+      for (int t = 0; t < ntiles; t += 2) {
+        step(st0, rs1, rs0, t);
+        step(st0, rs0, rs1, t + 1);
       }
     }
   }
@@ -328,7 +398,7 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) l_run[mt] = group4_allreduce_sum(l_run[mt]);
 
-  if (n_act <= 1) {
+  if (si.n_act <= 1) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int r = row0 + (wave * MT + mt) * 16 + l16;
@@ -346,7 +416,7 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
     return;
   }
 
-  // split: publish this workgroup's partial
+  // split: publish this workgroup's unnormalised partial for the combine kernel
   const int64_t slot = static_cast<int64_t>(unit) * p.n_splits + split;
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -356,60 +426,56 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
     for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16 + g * 4) = acc[mt][dt];
     if (g == 0) p.ws_ml[slot * p.rows_per_wg + rl] = make_float2(m_run[mt], l_run[mt]);
   }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const int prev = atomicAdd(&p.ws_cnt[unit], 1);
-    s_is_last = (prev == n_act - 1);
-  }
-  __syncthreads();
-  if (!s_is_last) return;
-  __threadfence();
+}
 
-  // last workgroup: merge n_act partials per row, 4 threads per row, D/4 columns each
-  constexpr int DQ = D / 4;
-  for (int rl = tid >> 2; rl < p.rows_per_wg; rl += kThreads / 4) {
-    const int r = row0 + rl;
-    if (r >= p.R) continue;
-    const int d0 = (tid & 3) * DQ;
-    float mmax = -INFINITY;
-    for (int sp = 0; sp < n_act; ++sp) {
-      const float2 ml = p.ws_ml[(static_cast<int64_t>(unit) * p.n_splits + sp) * p.rows_per_wg + rl];
-      mmax = fmaxf(mmax, ml.x);
-    }
-    const float m_use = mmax == -INFINITY ? 0.f : mmax;
-    float o[DQ];
+// Merge the split partials of every (sequence, KV head, row block) with more than
+// one active split. 8 output columns per thread, D / 8 threads per row.
+template <int D, bool F16, bool PAGED>
+__global__ __launch_bounds__(256) void kv_attn_combine_kernel(const AttnParams p) {
+  constexpr int TPR = D / 8;
+  constexpr int RPB = 256 / TPR;
+  const int unit = blockIdx.y;
+  const int bh = unit / p.n_rb;
+  const int rb = unit - bh * p.n_rb;
+  const int b = bh / p.Hkv;
+  const int kvh = bh - b * p.Hkv;
+  const SeqInfo si = seq_info<PAGED>(p, b, rb);
+  if (si.n_act <= 1) return;  // written directly by the attention kernel
+  const int rl = blockIdx.x * RPB + threadIdx.x / TPR;
+  const int r = rb * p.rows_per_wg + rl;
+  if (rl >= p.rows_per_wg || r >= p.R) return;
+  const int d0 = (threadIdx.x % TPR) * 8;
+  const int64_t base = static_cast<int64_t>(unit) * p.n_splits * p.rows_per_wg + rl;
+
+  float mmax = -INFINITY;
+#pragma unroll 4
+  for (int sp = 0; sp < si.n_act; ++sp) mmax = fmaxf(mmax, p.ws_ml[base + sp * p.rows_per_wg].x);
+  const float m_use = mmax == -INFINITY ? 0.f : mmax;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
+#pragma unroll 4
+  for (int sp = 0; sp < si.n_act; ++sp) {
+    const int64_t sl = base + sp * p.rows_per_wg;
+    const float2 ml = p.ws_ml[sl];
+    const f32x4* po = reinterpret_cast<const f32x4*>(p.ws_o + sl * D + d0);
+    const f32x4 x0 = po[0];
+    const f32x4 x1 = po[1];
+    const float w = exp2f(ml.x - m_use);
+    lsum += w * ml.y;
 #pragma unroll
-    for (int i = 0; i < DQ; ++i) o[i] = 0.f;
-    float lsum = 0.f;
-    for (int sp = 0; sp < n_act; ++sp) {
-      const int64_t sl = (static_cast<int64_t>(unit) * p.n_splits + sp) * p.rows_per_wg + rl;
-      const float2 ml = p.ws_ml[sl];
-      const float w = exp2f(ml.x - m_use);
-      lsum += w * ml.y;
-      const f32x4* po = reinterpret_cast<const f32x4*>(p.ws_o + sl * D + d0);
-#pragma unroll
-      for (int i = 0; i < DQ / 4; ++i) {
-        const f32x4 x = po[i];
-        o[4 * i + 0] += w * x[0];
-        o[4 * i + 1] += w * x[1];
-        o[4 * i + 2] += w * x[2];
-        o[4 * i + 3] += w * x[3];
-      }
-    }
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-    const int t = r / p.G;
-    const int hh = r - t * p.G;
-    uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh + d0;
-#pragma unroll
-    for (int i = 0; i < DQ / 8; ++i) {
-      u32x4 w4;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) w4[j] = pack2<F16>(o[8 * i + 2 * j] * inv, o[8 * i + 2 * j + 1] * inv);
-      *reinterpret_cast<u32x4*>(orow + 8 * i) = w4;
+    for (int j = 0; j < 4; ++j) {
+      o[j] += w * x0[j];
+      o[4 + j] += w * x1[j];
     }
   }
-  if (tid == 0) atomicExch(&p.ws_cnt[unit], 0);  // re-arm for the next call
+  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  const int t = r / p.G;
+  const int hh = r - t * p.G;
+  uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh + d0;
+  u32x4 w4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w4[j] = pack2<F16>(o[2 * j] * inv, o[2 * j + 1] * inv);
+  *reinterpret_cast<u32x4*>(orow) = w4;
 }
 
 // ---------------------------------------------------------------------------
@@ -468,16 +534,11 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const KVWriteArgs a) {
 // ---------------------------------------------------------------------------
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Workspace layout: a fixed header of completion counters, then the split-KV
-// partials. The header never holds partial data, so once zero-filled it stays
-// zero between calls (every completed call re-arms the counters it used), no
-// matter how the sizes of consecutive calls differ.
-constexpr size_t kCounterBytes = 16384;
-constexpr int64_t kMaxSplitUnits = kCounterBytes / sizeof(int);
-
+// Workspace layout: the (m, l) pairs of every split partial, then the partial
+// rows. Nothing needs to be zero: each call writes every slot it later reads.
 struct Plan {
   int MT, rows_per_wg, n_rb, n_splits, chunk, R;
-  size_t ws_o_bytes, ws_ml_bytes, ws_cnt_bytes;
+  size_t ws_o_bytes, ws_ml_bytes;
 };
 
 int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
@@ -495,8 +556,12 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
                   "fdllm_kv_attn: unknown mask_mode %d", d->mask_mode);
   FDLLM_CHECK_ARG(d->mask_mode != FDLLM_MASK_BLOCK_CAUSAL || d->mask_block > 0,
                   "fdllm_kv_attn: block-causal mask needs mask_block > 0");
-  FDLLM_CHECK_ARG(d->page_table == nullptr || (d->page_size > 0 && d->max_pages > 0),
-                  "fdllm_kv_attn: page table needs page_size > 0 and max_pages > 0");
+  // Each thread stages aligned groups of 2048 / head_dim keys from one page.
+  FDLLM_CHECK_ARG(d->page_table == nullptr ||
+                      (d->page_size >= kThreads * 8 / std::max(d->head_dim, 8) &&
+                       (d->page_size & (d->page_size - 1)) == 0 && d->max_pages > 0),
+                  "fdllm_kv_attn: page table needs a power-of-two page_size >= %d (got %d) and max_pages > 0",
+                  kThreads * 8 / std::max(d->head_dim, 8), d->page_size);
   FDLLM_CHECK_ARG(d->kv_split >= 0 && d->kv_split % kKT == 0, "fdllm_kv_attn: kv_split %d not a multiple of %d",
                   d->kv_split, kKT);
   const int G = d->num_q_heads / d->num_kv_heads;
@@ -527,15 +592,13 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
   }
   chunk_tiles = std::max(1, std::min(chunk_tiles, max_tiles));
   const int64_t units = static_cast<int64_t>(d->batch) * d->num_kv_heads * pl->n_rb;
-  if (units > kMaxSplitUnits) chunk_tiles = max_tiles;  // enough parallelism; no counters to spare
   pl->chunk = chunk_tiles * kKT;
   pl->n_splits = (max_tiles + chunk_tiles - 1) / chunk_tiles;
   if (pl->n_splits > 1) {
     pl->ws_o_bytes = static_cast<size_t>(units) * pl->n_splits * pl->rows_per_wg * d->head_dim * sizeof(float);
     pl->ws_ml_bytes = static_cast<size_t>(units) * pl->n_splits * pl->rows_per_wg * sizeof(float2);
-    pl->ws_cnt_bytes = kCounterBytes;
   } else {
-    pl->ws_o_bytes = pl->ws_ml_bytes = pl->ws_cnt_bytes = 0;
+    pl->ws_o_bytes = pl->ws_ml_bytes = 0;
   }
   return FDLLM_OK;
 }
@@ -544,10 +607,24 @@ inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255);
 
 template <int D, int MT>
 void launch_attn(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
+  const bool paged = p.page_table != nullptr;
   if (f16) {
-    kv_attn_kernel<D, MT, true><<<grid, dim3(kThreads), 0, s>>>(p);
+    if (paged) kv_attn_kernel<D, MT, true, true><<<grid, dim3(kThreads), 0, s>>>(p);
+    else kv_attn_kernel<D, MT, true, false><<<grid, dim3(kThreads), 0, s>>>(p);
   } else {
-    kv_attn_kernel<D, MT, false><<<grid, dim3(kThreads), 0, s>>>(p);
+    if (paged) kv_attn_kernel<D, MT, false, true><<<grid, dim3(kThreads), 0, s>>>(p);
+    else kv_attn_kernel<D, MT, false, false><<<grid, dim3(kThreads), 0, s>>>(p);
+  }
+  if (p.n_splits > 1) {
+    const int rpb = 256 / (D / 8);
+    const dim3 cgrid((p.rows_per_wg + rpb - 1) / rpb, grid.y * grid.z);
+    if (f16) {
+      if (paged) kv_attn_combine_kernel<D, true, true><<<cgrid, dim3(256), 0, s>>>(p);
+      else kv_attn_combine_kernel<D, true, false><<<cgrid, dim3(256), 0, s>>>(p);
+    } else {
+      if (paged) kv_attn_combine_kernel<D, false, true><<<cgrid, dim3(256), 0, s>>>(p);
+      else kv_attn_combine_kernel<D, false, false><<<cgrid, dim3(256), 0, s>>>(p);
+    }
   }
 }
 
@@ -560,7 +637,7 @@ extern "C" int fdllm_kv_attn_workspace_size(const fdllm_kv_attn_desc* desc, size
   Plan pl;
   const int rc = make_plan(desc, &pl);
   if (rc != FDLLM_OK) return rc;
-  *bytes = pl.n_splits > 1 ? align256(pl.ws_cnt_bytes) + align256(pl.ws_ml_bytes) + pl.ws_o_bytes : 0;
+  *bytes = pl.n_splits > 1 ? align256(pl.ws_ml_bytes) + pl.ws_o_bytes : 0;
   return FDLLM_OK;
 }
 
@@ -579,7 +656,7 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
                       d->v_stride_page % 8 == 0 && d->v_stride_slot % 8 == 0 && d->v_stride_h % 8 == 0 &&
                       d->out_stride_b % 8 == 0 && d->out_stride_s % 8 == 0 && d->out_stride_h % 8 == 0,
                   "fdllm_kv_attn_fwd: strides must be multiples of 8 elements");
-  const size_t need = pl.n_splits > 1 ? align256(pl.ws_cnt_bytes) + align256(pl.ws_ml_bytes) + pl.ws_o_bytes : 0;
+  const size_t need = pl.n_splits > 1 ? align256(pl.ws_ml_bytes) + pl.ws_o_bytes : 0;
   if (need > 0) {
     if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)) {
       set_last_error("fdllm_kv_attn_fwd: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
@@ -611,6 +688,8 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
   p.q_start = d->q_start;
   p.max_pages = d->max_pages;
   p.page_size = d->page_size;
+  p.page_shift = 0;
+  while (d->page_table && (1 << p.page_shift) < d->page_size) ++p.page_shift;
   p.max_seqlen = d->max_seqlen;
   p.B = d->batch;
   p.Sq = d->q_len;
@@ -627,11 +706,9 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
   p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
   if (need > 0) {
     char* w = static_cast<char*>(workspace);
-    p.ws_cnt = reinterpret_cast<int*>(w);
-    p.ws_ml = reinterpret_cast<float2*>(w + align256(pl.ws_cnt_bytes));
-    p.ws_o = reinterpret_cast<float*>(w + align256(pl.ws_cnt_bytes) + align256(pl.ws_ml_bytes));
+    p.ws_ml = reinterpret_cast<float2*>(w);
+    p.ws_o = reinterpret_cast<float*>(w + align256(pl.ws_ml_bytes));
   } else {
-    p.ws_cnt = nullptr;
     p.ws_ml = nullptr;
     p.ws_o = nullptr;
   }

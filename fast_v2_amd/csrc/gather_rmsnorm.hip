@@ -14,6 +14,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <type_traits>
+
 #include "fdllm_common.h"
 
 namespace fdllm {
@@ -75,40 +77,42 @@ struct Vec16<float> {
   __device__ __forceinline__ static float round(float x) { return x; }
 };
 
-// Load elements [e0, e0 + N) of the weight vector as fp32.
-template <int N>
-__device__ __forceinline__ void load_weight(const void* w, int wdtype, int e0, float* out) {
-  if (wdtype == FDLLM_DTYPE_F32) {
+// Weight kinds of the vector path: none, the 16-bit type of the rows (T), fp32.
+constexpr int kWNone = 0;
+constexpr int kW16 = 1;
+constexpr int kW32 = 2;
+
+// Load elements [e0, e0 + N) of the weight vector as fp32 (unconditional loads).
+template <typename T, int WK, int N>
+__device__ __forceinline__ void load_weight(const void* w, int e0, float* out) {
+  if constexpr (WK == kW32) {
     const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const float*>(w) + e0);
 #pragma unroll
     for (int i = 0; i < N / 4; ++i) {
-      u32x4 v = p[i];
+      const u32x4 v = p[i];
 #pragma unroll
       for (int j = 0; j < 4; ++j) out[4 * i + j] = __uint_as_float(v[j]);
     }
-  } else {
-    // 2-byte weights: N == 8 -> one 16-byte load, N == 4 -> one 8-byte load.
+  } else if constexpr (WK == kW16) {
     const uint16_t* base = static_cast<const uint16_t*>(w) + e0;
     uint32_t words[N / 2];
     if constexpr (N == 8) {
-      u32x4 v = *reinterpret_cast<const u32x4*>(base);
+      const u32x4 v = *reinterpret_cast<const u32x4*>(base);
 #pragma unroll
       for (int j = 0; j < 4; ++j) words[j] = v[j];
     } else {
-      u32x2 v = *reinterpret_cast<const u32x2*>(base);
+      const u32x2 v = *reinterpret_cast<const u32x2*>(base);
       words[0] = v[0];
       words[1] = v[1];
     }
 #pragma unroll
     for (int j = 0; j < N / 2; ++j) {
-      if (wdtype == FDLLM_DTYPE_BF16) {
-        out[2 * j] = Elt<bf16_t>::lo(words[j]);
-        out[2 * j + 1] = Elt<bf16_t>::hi(words[j]);
-      } else {
-        out[2 * j] = Elt<f16_t>::lo(words[j]);
-        out[2 * j + 1] = Elt<f16_t>::hi(words[j]);
-      }
+      out[2 * j] = Elt<T>::lo(words[j]);
+      out[2 * j + 1] = Elt<T>::hi(words[j]);
     }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = 1.f;
   }
 }
 
@@ -142,7 +146,7 @@ struct GatherArgs {
 
 // Vector path: H * sizeof(T) is a multiple of 16 and every row is 16-byte aligned.
 // VPL = 16-byte vectors per lane (the whole row stays in registers).
-template <typename T, int VPL>
+template <typename T, int WK, int VPL>
 __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArgs a) {
   constexpr int N = Vec16<T>::N;
   const int lane = threadIdx.x & (kWave - 1);
@@ -170,15 +174,18 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
   }
 
   const u32x4* hrow = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.hidden) + b * a.hs_b + src * a.hs_s);
+  // All loads are issued unconditionally (clamped index) and back to back, so the
+  // whole row is in flight at once; lanes past the row end are zeroed afterwards.
   u32x4 x[VPL];
 #pragma unroll
-  for (int v = 0; v < VPL; ++v) {
-    const int c = lane + kWave * v;
-    if (c < nvec) {
-      x[v] = hrow[c];
-    } else {
-      x[v] = u32x4{0u, 0u, 0u, 0u};
-    }
+  for (int v = 0; v < VPL; ++v) x[v] = hrow[min(lane + kWave * v, nvec - 1)];
+  float w[VPL][N];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) load_weight<T, WK, N>(a.weight, min(lane + kWave * v, nvec - 1) * N, w[v]);
+  if (nvec % kWave != 0) {
+#pragma unroll
+    for (int v = 0; v < VPL; ++v)
+      if (lane + kWave * v >= nvec) x[v] = u32x4{0u, 0u, 0u, 0u};
   }
 
   float ss = 0.f;
@@ -195,20 +202,14 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
     const int c = lane + kWave * v;
+    float f[N];
+    Vec16<T>::unpack(x[v], f);
+#pragma unroll
+    for (int i = 0; i < N; ++i) f[i] = apply_norm<T>(f[i], inv, w[v][i], a.mode);
+    const u32x4 o = Vec16<T>::pack(f);
     if (c < nvec) {
       if (grow) grow[c] = x[v];
-      float f[N];
-      Vec16<T>::unpack(x[v], f);
-      float w[N];
-      if (a.mode != FDLLM_NORM_PLAIN) {
-        load_weight<N>(a.weight, a.wdtype, c * N, w);
-      } else {
-#pragma unroll
-        for (int i = 0; i < N; ++i) w[i] = 1.f;
-      }
-#pragma unroll
-      for (int i = 0; i < N; ++i) f[i] = apply_norm<T>(f[i], inv, w[i], a.mode);
-      nrow[c] = Vec16<T>::pack(f);
+      nrow[c] = o;
     }
   }
 }
@@ -314,37 +315,53 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(const ScatterArgs a) 
   }
 }
 
+template <typename T, int WK>
+bool launch_gather_vec(const GatherArgs& a, dim3 grid, hipStream_t stream) {
+  const int nvec = a.H / Vec16<T>::N;
+  const int vpl = (nvec + kWave - 1) / kWave;
+  switch (vpl) {
+#define FDLLM_VPL_CASE(n)                                                  \
+  case n:                                                                  \
+    gather_rmsnorm_vec_kernel<T, WK, n><<<grid, dim3(256), 0, stream>>>(a); \
+    return true;
+    FDLLM_VPL_CASE(1)
+    FDLLM_VPL_CASE(2)
+    FDLLM_VPL_CASE(3)
+    FDLLM_VPL_CASE(4)
+    FDLLM_VPL_CASE(5)
+    FDLLM_VPL_CASE(6)
+    FDLLM_VPL_CASE(7)
+    FDLLM_VPL_CASE(8)
+    FDLLM_VPL_CASE(10)
+    FDLLM_VPL_CASE(12)
+    FDLLM_VPL_CASE(14)
+    FDLLM_VPL_CASE(16)
+#undef FDLLM_VPL_CASE
+    default:
+      return false;  // uneven or very wide rows: generic path
+  }
+}
+
 template <typename T>
 int launch_gather(const GatherArgs& a, bool vec, hipStream_t stream) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.T;
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
-  const dim3 block(256);
   if (vec) {
-    const int nvec = a.H / Vec16<T>::N;
-    const int vpl = (nvec + kWave - 1) / kWave;
-    switch (vpl) {
-#define FDLLM_VPL_CASE(n) \
-  case n:                 \
-    gather_rmsnorm_vec_kernel<T, n><<<grid, block, 0, stream>>>(a); \
-    return 0;
-      FDLLM_VPL_CASE(1)
-      FDLLM_VPL_CASE(2)
-      FDLLM_VPL_CASE(3)
-      FDLLM_VPL_CASE(4)
-      FDLLM_VPL_CASE(5)
-      FDLLM_VPL_CASE(6)
-      FDLLM_VPL_CASE(7)
-      FDLLM_VPL_CASE(8)
-      FDLLM_VPL_CASE(10)
-      FDLLM_VPL_CASE(12)
-      FDLLM_VPL_CASE(14)
-      FDLLM_VPL_CASE(16)
-#undef FDLLM_VPL_CASE
-      default:
-        break;  // uneven or very wide rows: generic path
+    bool done;
+    if (a.mode == FDLLM_NORM_PLAIN) {
+      done = launch_gather_vec<T, kWNone>(a, grid, stream);
+    } else if (a.wdtype == FDLLM_DTYPE_F32) {
+      done = launch_gather_vec<T, kW32>(a, grid, stream);
+    } else if constexpr (!std::is_same<T, float>::value) {
+      // 16-bit weights in the rows' own format; other combinations take the generic path
+      const bool same = (a.wdtype == FDLLM_DTYPE_BF16) == std::is_same<T, bf16_t>::value;
+      done = same && launch_gather_vec<T, kW16>(a, grid, stream);
+    } else {
+      done = false;
     }
+    if (done) return 0;
   }
-  gather_rmsnorm_generic_kernel<T><<<grid, block, 0, stream>>>(a);
+  gather_rmsnorm_generic_kernel<T><<<grid, dim3(256), 0, stream>>>(a);
   return 0;
 }
 

@@ -129,6 +129,8 @@ int fdllm_scatter_rows(const void* values, const int64_t* indices, int64_t indic
  * with (page, slot) = (page_table[b * max_pages + j / page_size], j % page_size)
  * when page_table != NULL, else (b, j): the contiguous [batch, max_S, Hkv, D]
  * static cache of static_kv_cache.py:55-69 is the page-table-free case.
+ * page_size must be a power of two, at least 16 for head_dim 128 and at least
+ * 32 for head_dim 64.
  * ------------------------------------------------------------------------- */
 typedef struct fdllm_kv_attn_desc {
   const void* q; /* [batch, q_len, num_q_heads, head_dim] */

@@ -209,3 +209,22 @@ def test_workspace_reuse_across_shapes(gpu):
         out = ops.block_attn(wl.q.to(gpu), kc, vc, sl, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL,
                              mask_block=wl.block, kv_split=split)
         _check(out, exp)
+
+
+@pytest.mark.parametrize("page_size", [16, 64, 256])
+def test_page_sizes(gpu, page_size):
+    wl = workloads.kv_decode_paged(seed=5, batch=5, min_prefix=96, max_prefix=1500, page_size=page_size)
+    print(f"case page_size={page_size} lens={wl.seqlens.tolist()}", flush=True)
+    for split in (0, 128):
+        out = ops.block_attn(wl.q.to(gpu), wl.k_pool.to(gpu), wl.v_pool.to(gpu), wl.seqlens.to(gpu), wl.scale,
+                             page_table=wl.page_table.to(gpu), page_size=page_size, kv_split=split)
+        exp = oa.attention_np(wl.q.float(), wl.k_pool.float(), wl.v_pool.float(), wl.seqlens, wl.scale,
+                              page_table=wl.page_table, page_size=page_size)
+        _check(out, exp)
+
+
+def test_bad_page_size_rejected(gpu):
+    wl = workloads.kv_decode_paged(seed=5, batch=2, min_prefix=96, max_prefix=200, page_size=48)
+    with pytest.raises(RuntimeError, match="page_size"):
+        ops.block_attn(wl.q.to(gpu), wl.k_pool.to(gpu), wl.v_pool.to(gpu), wl.seqlens.to(gpu), wl.scale,
+                       page_table=wl.page_table.to(gpu), page_size=48)
