@@ -110,7 +110,7 @@ def bench_decode(torch, args):
     pt = wl.page_table.to(dev)
     sl = wl.seqlens.to(dev)
     page_size = wl.page_size
-    if args.layout == "contig":
+    if args.layout in ("contig", "bhsd"):
         # the reference's static cache layout [B, max_S, Hkv, D] per layer (identity pages)
         B = q.shape[0]
         max_s = int(wl.seqlens.max())
@@ -118,6 +118,10 @@ def bench_decode(torch, args):
         idx = pt[:, (pos // page_size).clamp(max=pt.shape[1] - 1)].long()  # [B, max_S]
         kc = kp[:, idx, pos % page_size]  # [layers, B, max_S, Hkv, D]
         vc = vp[:, idx, pos % page_size]
+        if args.layout == "bhsd":
+            # head-major storage [layers, B, Hkv, max_S, D] viewed as [layers, B, max_S, Hkv, D]
+            kc = kc.permute(0, 1, 3, 2, 4).contiguous().permute(0, 1, 3, 2, 4)
+            vc = vc.permute(0, 1, 3, 2, 4).contiguous().permute(0, 1, 3, 2, 4)
         kp, vp, pt, page_size = kc, vc, None, 0
         torch.cuda.empty_cache()
     _log(f"decode: lens={wl.seqlens.tolist()} layout={args.layout} "
@@ -280,8 +284,9 @@ def main() -> int:
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--kv-split", type=int, default=0, help="keys per split-KV work item (0 = automatic)")
     ap.add_argument("--layers", type=int, default=LAYERS, help="layer pools cycled by the decode steps")
-    ap.add_argument("--layout", choices=["paged", "contig"], default="paged",
-                    help="KV layout: 32-token pages, or the contiguous [B, max_S, Hkv, D] static cache")
+    ap.add_argument("--layout", choices=["paged", "contig", "bhsd"], default="paged",
+                    help="KV layout: 32-token pages, the contiguous [B, max_S, Hkv, D] static cache, "
+                         "or the same cache stored head-major")
     ap.add_argument("--no-check", action="store_true", help="skip the graph-vs-eager equality check")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")

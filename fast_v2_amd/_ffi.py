@@ -59,7 +59,11 @@ class KVAttnDesc(ctypes.Structure):
         ("head_dim", _c_i32),
         ("mask_mode", _c_i32), ("mask_block", _c_i32), ("dtype", _c_i32), ("kv_split", _c_i32),
         ("softmax_scale", _c_float),
+        ("flags", _c_i32),
     ]
+
+
+ATTN_NO_DECODE_KERNEL = 1
 
 
 # name -> (restype, argtypes); every symbol of include/fdllm_hip.h

@@ -42,6 +42,7 @@ namespace fdllm {
 namespace {
 
 constexpr int kKT = 64;        // keys per tile
+constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 (gfx9: 32-bit data format)
 constexpr int kThreads = 256;  // 4 waves
 
 struct AttnParams {
@@ -87,6 +88,18 @@ __device__ __forceinline__ uint32_t pack2(float a, float b) {
   } else {
     return Elt<bf16_t>::pack(a, b);
   }
+}
+
+// 2^x with the hardware transcendental (v_exp_f32): no denormal range fix-up;
+// exp2(-inf) = 0, the softmax's masked value.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+
+// ds_read_b64_tr_b16: transposing LDS read of four 16-bit values (see kv_decode_kernel).
+__device__ __forceinline__ s16x4 lds_read_tr16(const uint16_t* lds_ptr) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr));
 }
 
 // Workgroup barrier that orders LDS only: waits for this wave's LDS operations,
@@ -135,7 +148,7 @@ __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b, int rb) 
 }
 
 template <int D, int MT, bool F16, bool PAGED>
-__global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
+__global__ __launch_bounds__(kThreads, MT <= 2 ? 2 : 1) void kv_attn_kernel(const AttnParams p) {
   constexpr int KS = D + 8;      // K row stride in LDS (elements), 16-byte pad
   constexpr int VS = kKT + 4;    // V^T row stride in LDS (elements), 8-byte pad
   constexpr int NKS = D / 32;    // MFMA k-steps over d for S
@@ -175,11 +188,18 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
     const int rc = min(r, p.R - 1);  // padding rows read a valid row; their limit is 0
     const int t = rc / p.G;
     const int hh = rc - t * p.G;
-    lim[mt] = r < p.R ? row_key_limit(p, si.seqlen, si.qs, t) : 0;
+    // padding rows (r >= R) reuse a valid row's query and limit: finite, never written
+    lim[mt] = row_key_limit(p, si.seqlen, si.qs, t);
     const uint16_t* qrow = p.q + b * p.q_sb + t * p.q_ss + (kvh * p.G + hh) * p.q_sh;
 #pragma unroll
     for (int ks = 0; ks < NKS; ++ks) qf[mt][ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 32 + g * 8);
   }
+
+  // tiles wholly below every row limit of this wave need no mask
+  int lim_min = lim[0];
+#pragma unroll
+  for (int mt = 1; mt < MT; ++mt) lim_min = min(lim_min, lim[mt]);
+  lim_min = __builtin_amdgcn_readfirstlane(-static_cast<int>(wave_allreduce_max(-static_cast<float>(lim_min))));
 
   f32x4 acc[MT][NDT];
   float m_run[MT], l_run[MT];
@@ -293,39 +313,47 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
         s[mt][st] = c;
       }
     }
-    // lane owns query row l16 of each M-tile; its 16 scores sit at keys kb + 16st + 4g + j
+    // lane owns query row l16 of each M-tile; its 16 scores sit at keys kb + 16st + 4g + j.
+    // Scores stay unscaled; scale * log2(e) is folded into the exponent's FMA.
+    const bool full_tile = kb + kKT <= lim_min;  // wave-uniform
     u32x4 pf[MT][2];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
+      if (!full_tile) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (kb + st * 16 + g * 4 + j >= lim[mt]) s[mt][st][j] = -INFINITY;
+      }
       float tmax = -INFINITY;
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
+      for (int st = 0; st < 4; ++st)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int key = kb + st * 16 + g * 4 + j;
-          const float x = key < lim[mt] ? s[mt][st][j] * p.scale_log2 : -INFINITY;
-          s[mt][st][j] = x;
-          tmax = fmaxf(tmax, x);
-        }
-      }
+        for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, s[mt][st][j]);
       tmax = group4_allreduce_max(tmax);
       const float m_new = fmaxf(m_run[mt], tmax);
-      const float m_use = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = exp2f(m_run[mt] - m_use);
-      m_run[mt] = m_new;
+      // Rescale the accumulators only when some lane's running max moved; alpha is
+      // exactly 1 for every other lane, so skipping is exact.
+      if (__builtin_amdgcn_ballot_w64(m_new > m_run[mt]) != 0) {
+        const float alpha = m_new == -INFINITY ? 1.f : fast_exp2((m_run[mt] - m_new) * p.scale_log2);
+        l_run[mt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[mt][dt] *= alpha;
+        m_run[mt] = m_new;
+      }
+      const float mc = m_new == -INFINITY ? 0.f : m_new * p.scale_log2;
       float lsum = 0.f;
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          const float e = exp2f(s[mt][st][j] - m_use);
+          const float e = fast_exp2(fmaf(s[mt][st][j], p.scale_log2, -mc));
           s[mt][st][j] = e;
           lsum += e;
         }
       }
-      l_run[mt] = l_run[mt] * alpha + lsum;
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) acc[mt][dt] *= alpha;
+      l_run[mt] += lsum;
       // B operand of O^T = V^T P^T for key steps kk = 0, 1:
       // k-index 8g + j <-> key 32kk + 4g + j (j < 4), 32kk + 16 + 4g + (j - 4) (j >= 4)
 #pragma unroll
@@ -428,12 +456,272 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(const AttnParams p) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Decode-shaped attention: every KV head of a key range in one workgroup.
+//
+// For q_len * G <= 64 rows per KV head and head_dim 128 with the heads of one
+// key stored next to each other (the [.., Hkv, D] cache rows of
+// static_kv_cache.py, or a page pool [pages, page_size, Hkv, D]), a workgroup of
+// 2 * HKV waves streams whole key rows (HKV * 256 bytes) of its split: each
+// 16-byte load instruction of a wave covers one contiguous row, which is what
+// HBM serves best, and every byte feeds the G query heads of its KV head.
+//   * Tiles of 32 keys; K and V land in LDS row-major with plain 16-byte stores.
+//   * Wave w works on KV head w / 2, query rows 32 * (w % 2) .. +32 (2 M-tiles).
+//   * S^T = K Q^T as in kv_attn_kernel; the V^T operand of O^T = V^T P^T is read
+//     with ds_read_b64_tr_b16 (gfx950 LDS transpose read): in each 16-lane group,
+//     lane j receives element j % 4 of lanes 4k + j / 4 (k = 0..3), so a lane
+//     addressing V[kb + l16 / 4][16 dt + 4 (l16 % 4)] receives the four keys
+//     kb .. kb + 3 at d = 16 dt + l16.
+//   * Partials use the layout of kv_attn_kernel with rows_per_wg = 64, so the
+//     same combine kernel merges the splits.
+template <int HKV, bool F16, bool PAGED>
+__global__ __launch_bounds__(128 * HKV) void kv_decode_kernel(const AttnParams p) {
+  constexpr int D = 128;
+  constexpr int NT = 128 * HKV;
+  constexpr int KT = 32;
+  constexpr int ROWE = HKV * D;       // elements of one key row (all heads)
+  constexpr int KS = ROWE + 8;        // K row stride in LDS: +16 bytes (conflict-free b128 reads)
+  constexpr int VS = ROWE + 16;       // V row stride in LDS: +32 bytes (conflict-free transpose reads)
+  constexpr int CPR = ROWE / 8;       // 16-byte chunks per key row
+  constexpr int LPT = KT * CPR / NT;  // 16-byte loads per thread per tile, per tensor
+  constexpr int NDT = D / 16;
+  static_assert(LPT == 4, "tile shape");
+  __shared__ __attribute__((aligned(16))) uint16_t sK[KT * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t sV[KT * VS];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+  const int h = wave >> 1;
+  const int half = wave & 1;
+
+  const int split = blockIdx.x;
+  const int b = blockIdx.y;
+  const SeqInfo si = seq_info<PAGED>(p, b, 0);
+  if (split >= max(si.n_act, 1)) return;
+  const int k_lo = split * p.chunk;
+  const int k_hi = min(si.kv_end, k_lo + p.chunk);
+  const int ntiles = k_hi > k_lo ? (k_hi - k_lo + KT - 1) / KT : 0;
+
+  // ---- query fragments of this wave's 32 rows (2 M-tiles) of head h
+  u32x4 qf[2][4];
+  int lim[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int r = half * 32 + mt * 16 + l16;
+    const int rc = min(r, p.R - 1);  // padding rows reuse a valid row: finite, never written
+    const int t = rc / p.G;
+    const int hh = rc - t * p.G;
+    lim[mt] = row_key_limit(p, si.seqlen, si.qs, t);
+    const uint16_t* qrow = p.q + b * p.q_sb + t * p.q_ss + (h * p.G + hh) * p.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[mt][ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 32 + g * 8);
+  }
+  int lim_min = min(lim[0], lim[1]);
+  lim_min = __builtin_amdgcn_readfirstlane(-static_cast<int>(wave_allreduce_max(-static_cast<float>(lim_min))));
+  const float rescale_thr = 8.f / p.scale_log2;  // raw-score distance of a 2^8 factor
+
+  f32x4 acc[2][NDT];
+  float m_run[2], l_run[2];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    m_run[mt] = -INFINITY;
+    l_run[mt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[mt][dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  // ---- staging: chunk c = tid + NT * i of the tile -> key c / CPR, column (c % CPR) * 8.
+  // Buffer loads: the descriptor (scalar) points at the tile's first key and covers
+  // only the keys below k_hi, so keys past the end read as zero with no clamping;
+  // each thread's byte offsets inside a tile are the same for every tile.
+  struct Stage {
+    u32x4 k[LPT];
+    u32x4 v[LPT];
+  };
+  Stage st0, st1;
+  const int32_t* pt_row = PAGED ? p.page_table + static_cast<int64_t>(b) * p.max_pages : nullptr;
+  const int krow_bytes = static_cast<int>(p.k_ss) * 2;
+  const int vrow_bytes = static_cast<int>(p.v_ss) * 2;
+  int koff[LPT], voff[LPT];
+#pragma unroll
+  for (int i = 0; i < LPT; ++i) {
+    const int c = tid + NT * i;
+    koff[i] = (c / CPR) * krow_bytes + (c % CPR) * 16;
+    voff[i] = (c / CPR) * vrow_bytes + (c % CPR) * 16;
+  }
+  auto load_tile = [&](Stage& st, int kb) {
+    // every value the descriptors are built from is wave-uniform; readfirstlane
+    // states it, so the descriptors live in scalar registers
+    const int valid = __builtin_amdgcn_readfirstlane(max(0, min(KT, k_hi - kb)));
+    const uint16_t* kt;
+    const uint16_t* vt;
+    if constexpr (PAGED) {
+      // a 32-key tile lies in one page (page_size is a power of two >= 32)
+      const int page = __builtin_amdgcn_readfirstlane(pt_row[min(kb, k_hi - 1) >> p.page_shift]);
+      const int slot0 = kb & (p.page_size - 1);
+      kt = p.k + static_cast<int64_t>(page) * p.k_sp + static_cast<int64_t>(slot0) * p.k_ss;
+      vt = p.v + static_cast<int64_t>(page) * p.v_sp + static_cast<int64_t>(slot0) * p.v_ss;
+    } else {
+      kt = p.k + b * p.k_sp + static_cast<int64_t>(kb) * p.k_ss;
+      vt = p.v + b * p.v_sp + static_cast<int64_t>(kb) * p.v_ss;
+    }
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kt), 0, valid * krow_bytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vt), 0, valid * vrow_bytes, kBufferFlags);
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      st.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0));
+      st.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, 0));
+    }
+  };
+  auto store_tile = [&](const Stage& st) {
+#pragma unroll
+    for (int i = 0; i < LPT; ++i) {
+      const int c = tid + NT * i;
+      *reinterpret_cast<u32x4*>(&sK[(c / CPR) * KS + (c % CPR) * 8]) = st.k[i];
+      *reinterpret_cast<u32x4*>(&sV[(c / CPR) * VS + (c % CPR) * 8]) = st.v[i];
+    }
+  };
+
+  auto compute_tile = [&](int kb) {
+    // S^T for two 16-key sub-tiles
+    f32x4 s[2][2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      u32x4 kf[4];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        kf[ks] = *reinterpret_cast<const u32x4*>(&sK[(st * 16 + l16) * KS + h * D + ks * 32 + g * 8]);
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) c = mfma16x16x32<F16>(kf[ks], qf[mt][ks], c);
+        s[mt][st] = c;
+      }
+    }
+    const bool full_tile = kb + KT <= lim_min;  // wave-uniform
+    u32x4 pf[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      if (!full_tile) {
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (kb + st * 16 + g * 4 + j >= lim[mt]) s[mt][st][j] = -INFINITY;
+      }
+      float tmax = -INFINITY;
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, s[mt][st][j]);
+      tmax = group4_allreduce_max(tmax);
+      // The reference max m_run only moves when a score exceeds it by more than
+      // 2^8 in the exponent (or on the first visible key): exponentials stay <= 256,
+      // far from fp32 / bf16 overflow, and the result is the same function.
+      if (__builtin_amdgcn_ballot_w64(tmax > m_run[mt] + rescale_thr) != 0) {
+        const float m_new = fmaxf(m_run[mt], tmax);
+        const float alpha = m_run[mt] == -INFINITY ? 0.f : fast_exp2((m_run[mt] - m_new) * p.scale_log2);
+        l_run[mt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[mt][dt] *= alpha;
+        m_run[mt] = m_new;
+      }
+      const float mc = m_run[mt] == -INFINITY ? 0.f : m_run[mt] * p.scale_log2;
+      float lsum = 0.f;
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float e = fast_exp2(fmaf(s[mt][st][j], p.scale_log2, -mc));
+          s[mt][st][j] = e;
+          lsum += e;
+        }
+      }
+      l_run[mt] += lsum;
+      // k-index 8g + j <-> key 4g + j (j < 4), 16 + 4g + (j - 4) (j >= 4)
+      pf[mt][0] = pack2<F16>(s[mt][0][0], s[mt][0][1]);
+      pf[mt][1] = pack2<F16>(s[mt][0][2], s[mt][0][3]);
+      pf[mt][2] = pack2<F16>(s[mt][1][0], s[mt][1][1]);
+      pf[mt][3] = pack2<F16>(s[mt][1][2], s[mt][1][3]);
+    }
+    // O^T += V^T P^T; V^T fragments by LDS transpose reads of row-major V
+    const int vrow = 4 * g + (l16 >> 2);
+    const int vcol = h * D + 4 * (l16 & 3);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const s16x4 lo = lds_read_tr16(&sV[vrow * VS + vcol + dt * 16]);
+      const s16x4 hi = lds_read_tr16(&sV[(vrow + 16) * VS + vcol + dt * 16]);
+      const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
+      const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
+      const u32x4 vf = {lo2[0], lo2[1], hi2[0], hi2[1]};
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) acc[mt][dt] = mfma16x16x32<F16>(vf, pf[mt], acc[mt][dt]);
+    }
+  };
+
+  // Two tiles in flight (see kv_attn_kernel): every step issues the same loads,
+  // zero-filled past k_hi, so the waits stay exact; only the math is conditional.
+  auto step = [&](Stage& st, int t) {
+    lds_barrier();
+    store_tile(st);
+    lds_barrier();
+    load_tile(st, k_lo + (t + 2) * KT);
+    if (t < ntiles) compute_tile(k_lo + t * KT);
+  };
+  if (ntiles > 0) {
+    load_tile(st0, k_lo);
+    load_tile(st1, k_lo + KT);
+    for (int t = 0; t < ntiles; t += 2) {
+      step(st0, t);
+      step(st1, t + 1);
+    }
+  }
+
+  // ---- epilogue
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) l_run[mt] = group4_allreduce_sum(l_run[mt]);
+  if (si.n_act <= 1) {
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int r = half * 32 + mt * 16 + l16;
+      if (r >= p.R) continue;
+      const int t = r / p.G;
+      const int hh = r - t * p.G;
+      const float inv = l_run[mt] > 0.f ? 1.f / l_run[mt] : 0.f;
+      uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (h * p.G + hh) * p.o_sh;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const f32x4 o = acc[mt][dt] * inv;
+        *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) = u32x2{pack2<F16>(o[0], o[1]), pack2<F16>(o[2], o[3])};
+      }
+    }
+    return;
+  }
+  const int64_t slot = static_cast<int64_t>(b * p.Hkv + h) * p.n_splits + split;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int rl = half * 32 + mt * 16 + l16;
+    if (rl >= p.R) continue;  // padding rows are never read
+    float* po = p.ws_o + (slot * 64 + rl) * D;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16 + g * 4) = acc[mt][dt];
+    if (g == 0) p.ws_ml[slot * 64 + rl] = make_float2(m_run[mt], l_run[mt]);
+  }
+}
+
 // Merge the split partials of every (sequence, KV head, row block) with more than
 // one active split. 8 output columns per thread, D / 8 threads per row.
 template <int D, bool F16, bool PAGED>
 __global__ __launch_bounds__(256) void kv_attn_combine_kernel(const AttnParams p) {
   constexpr int TPR = D / 8;
   constexpr int RPB = 256 / TPR;
+  constexpr int U = 4;  // splits whose loads are in flight together
   const int unit = blockIdx.y;
   const int bh = unit / p.n_rb;
   const int rb = unit - bh * p.n_rb;
@@ -447,28 +735,37 @@ __global__ __launch_bounds__(256) void kv_attn_combine_kernel(const AttnParams p
   const int d0 = (threadIdx.x % TPR) * 8;
   const int64_t base = static_cast<int64_t>(unit) * p.n_splits * p.rows_per_wg + rl;
 
-  float mmax = -INFINITY;
-#pragma unroll 4
-  for (int sp = 0; sp < si.n_act; ++sp) mmax = fmaxf(mmax, p.ws_ml[base + sp * p.rows_per_wg].x);
-  const float m_use = mmax == -INFINITY ? 0.f : mmax;
+  // online merge: m = running reference max, l / o scaled to it
+  float m = -INFINITY, l = 0.f;
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;
-#pragma unroll 4
-  for (int sp = 0; sp < si.n_act; ++sp) {
-    const int64_t sl = base + sp * p.rows_per_wg;
-    const float2 ml = p.ws_ml[sl];
-    const f32x4* po = reinterpret_cast<const f32x4*>(p.ws_o + sl * D + d0);
-    const f32x4 x0 = po[0];
-    const f32x4 x1 = po[1];
-    const float w = exp2f(ml.x - m_use);
-    lsum += w * ml.y;
+  for (int sp0 = 0; sp0 < si.n_act; sp0 += U) {
+    float2 ml[U];
+    f32x4 x0[U], x1[U];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      o[j] += w * x0[j];
-      o[4 + j] += w * x1[j];
+    for (int u = 0; u < U; ++u) {
+      const int64_t sl = base + static_cast<int64_t>(min(sp0 + u, si.n_act - 1)) * p.rows_per_wg;
+      ml[u] = p.ws_ml[sl];
+      const f32x4* po = reinterpret_cast<const f32x4*>(p.ws_o + sl * D + d0);
+      x0[u] = po[0];
+      x1[u] = po[1];
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (sp0 + u >= si.n_act) break;
+      const float mn = fmaxf(m, ml[u].x);
+      if (mn == -INFINITY) continue;  // neither side has a visible key yet
+      const float a = m == -INFINITY ? 0.f : fast_exp2((m - mn) * p.scale_log2);
+      const float w = ml[u].x == -INFINITY ? 0.f : fast_exp2((ml[u].x - mn) * p.scale_log2);
+      l = l * a + w * ml[u].y;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        o[j] = o[j] * a + w * x0[u][j];
+        o[4 + j] = o[4 + j] * a + w * x1[u][j];
+      }
+      m = mn;
     }
   }
-  const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+  const float inv = l > 0.f ? 1.f / l : 0.f;
   const int t = r / p.G;
   const int hh = r - t * p.G;
   uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh + d0;
@@ -537,6 +834,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // Workspace layout: the (m, l) pairs of every split partial, then the partial
 // rows. Nothing needs to be zero: each call writes every slot it later reads.
 struct Plan {
+  bool decode;  // all-heads decode kernel (kv_decode_kernel)
   int MT, rows_per_wg, n_rb, n_splits, chunk, R;
   size_t ws_o_bytes, ws_ml_bytes;
 };
@@ -568,6 +866,38 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
   const int64_t R64 = static_cast<int64_t>(d->q_len) * G;
   FDLLM_CHECK_ARG(R64 < (1 << 30), "fdllm_kv_attn: q_len * group too large");
   pl->R = static_cast<int>(R64);
+  const int hkv = d->num_kv_heads;
+  pl->decode = !(d->flags & FDLLM_ATTN_NO_DECODE_KERNEL) && d->head_dim == 128 && pl->R <= 64 &&
+               (hkv == 1 || hkv == 2 || hkv == 4 || hkv == 8) && d->k_stride_h == 128 && d->v_stride_h == 128 &&
+               (d->page_table == nullptr || d->page_size >= 32);
+  if (pl->decode) {
+    const int max_len = d->page_table
+                            ? std::min<int64_t>(d->max_seqlen, static_cast<int64_t>(d->max_pages) * d->page_size)
+                            : d->max_seqlen;
+    const int max_t32 = std::max(1, (max_len + 31) / 32);
+    int chunk_t32;
+    if (d->kv_split > 0) {
+      chunk_t32 = d->kv_split / 32;
+    } else {
+      // ~320 workgroups when every sequence is full length, >= 128 keys each
+      const int64_t splits = (320 + std::max(d->batch, 1) - 1) / std::max(d->batch, 1);
+      chunk_t32 = std::max<int>(4, static_cast<int>((max_t32 + splits - 1) / splits));
+    }
+    chunk_t32 = std::max(1, std::min(chunk_t32, max_t32));
+    pl->MT = 0;
+    pl->rows_per_wg = 64;
+    pl->n_rb = 1;
+    pl->chunk = chunk_t32 * 32;
+    pl->n_splits = (max_t32 + chunk_t32 - 1) / chunk_t32;
+    const int64_t units = static_cast<int64_t>(d->batch) * hkv;
+    if (pl->n_splits > 1) {
+      pl->ws_o_bytes = static_cast<size_t>(units) * pl->n_splits * 64 * d->head_dim * sizeof(float);
+      pl->ws_ml_bytes = static_cast<size_t>(units) * pl->n_splits * 64 * sizeof(float2);
+    } else {
+      pl->ws_o_bytes = pl->ws_ml_bytes = 0;
+    }
+    return FDLLM_OK;
+  }
   const int mtiles = (pl->R + 15) / 16;
   pl->MT = mtiles <= 4 ? 1 : (mtiles <= 8 ? 2 : 4);
   pl->rows_per_wg = 64 * pl->MT;
@@ -604,6 +934,37 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
 }
 
 inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+
+template <int D, bool F16, bool PAGED>
+void launch_combine(const AttnParams& p, unsigned units, hipStream_t s) {
+  const int rpb = 256 / (D / 8);
+  const dim3 cgrid((p.rows_per_wg + rpb - 1) / rpb, units);
+  kv_attn_combine_kernel<D, F16, PAGED><<<cgrid, dim3(256), 0, s>>>(p);
+}
+
+template <int HKV>
+void launch_decode(const AttnParams& p, bool f16, hipStream_t s) {
+  const bool paged = p.page_table != nullptr;
+  const dim3 grid(p.n_splits, p.B);
+  const dim3 block(128 * HKV);
+  if (f16) {
+    if (paged) kv_decode_kernel<HKV, true, true><<<grid, block, 0, s>>>(p);
+    else kv_decode_kernel<HKV, true, false><<<grid, block, 0, s>>>(p);
+  } else {
+    if (paged) kv_decode_kernel<HKV, false, true><<<grid, block, 0, s>>>(p);
+    else kv_decode_kernel<HKV, false, false><<<grid, block, 0, s>>>(p);
+  }
+  if (p.n_splits > 1) {
+    const unsigned units = static_cast<unsigned>(p.B * HKV);
+    if (f16) {
+      if (paged) launch_combine<128, true, true>(p, units, s);
+      else launch_combine<128, true, false>(p, units, s);
+    } else {
+      if (paged) launch_combine<128, false, true>(p, units, s);
+      else launch_combine<128, false, false>(p, units, s);
+    }
+  }
+}
 
 template <int D, int MT>
 void launch_attn(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
@@ -712,9 +1073,18 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
     p.ws_ml = nullptr;
     p.ws_o = nullptr;
   }
-  const dim3 grid(pl.n_splits, pl.n_rb, static_cast<unsigned>(grid_z));
   const bool f16 = d->dtype == FDLLM_DTYPE_F16;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.decode) {
+    switch (d->num_kv_heads) {
+      case 1: launch_decode<1>(p, f16, s); break;
+      case 2: launch_decode<2>(p, f16, s); break;
+      case 4: launch_decode<4>(p, f16, s); break;
+      default: launch_decode<8>(p, f16, s); break;
+    }
+    FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
+  }
+  const dim3 grid(pl.n_splits, pl.n_rb, static_cast<unsigned>(grid_z));
   if (d->head_dim == 128) {
     if (pl.MT == 1) launch_attn<128, 1>(p, f16, grid, s);
     else if (pl.MT == 2) launch_attn<128, 2>(p, f16, grid, s);

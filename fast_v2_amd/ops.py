@@ -48,11 +48,11 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 class _Workspace:
-    """Zero-filled scratch per (device, stream), grown on demand and reused.
+    """Scratch per (device, stream), grown on demand and reused.
 
-    The split-KV attention leaves its workspace ready for the next call (its
-    completion counters are re-armed by the kernel), so the buffer is cleared
-    only when it is first allocated.
+    The split-KV attention writes every partial it later merges, so the buffer
+    needs no clearing between calls; calls on one stream run in order and may
+    share it.
     """
 
     def __init__(self) -> None:
@@ -151,7 +151,7 @@ def scatter_rows(values: torch.Tensor, indices: torch.Tensor,
 # ---------------------------------------------------------------------------
 
 def _attn_desc(q, k_cache, v_cache, seqlens, out, scale, mask_mode, mask_block,
-               q_start, page_table, page_size, kv_split) -> _ffi.KVAttnDesc:
+               q_start, page_table, page_size, kv_split, flags=0) -> _ffi.KVAttnDesc:
     B, Sq, Hq, D = q.shape
     d = _ffi.KVAttnDesc()
     d.q = q.data_ptr()
@@ -180,6 +180,7 @@ def _attn_desc(q, k_cache, v_cache, seqlens, out, scale, mask_mode, mask_block,
     d.dtype = _ffi.dtype_code(q.dtype)
     d.kv_split = int(kv_split)
     d.softmax_scale = float(scale)
+    d.flags = int(flags)
     return d
 
 
@@ -196,6 +197,7 @@ def block_attn(
     page_size: int = 0,
     out: Optional[torch.Tensor] = None,
     kv_split: int = 0,
+    decode_kernel: bool = True,
 ) -> torch.Tensor:
     """Attention of BSHD queries over a (paged) BSHD KV cache.
 
@@ -204,6 +206,8 @@ def block_attn(
                  [num_pages, page_size, Hkv, D] with ``page_table`` [B, max_pages] int32
     cache_seqlens [B] visible key count per sequence (int32; other ints converted)
     Returns a new [B, Sq, Hq, D] tensor (or fills ``out``).
+    decode_kernel=False forces the general kernel where the all-heads decode
+    kernel would apply (both compute the same function).
     """
     if q.dim() != 4 or k_cache.dim() != 4 or v_cache.dim() != 4:
         raise RuntimeError("block_attn: q, k_cache and v_cache must be 4-D (BSHD)")
@@ -245,7 +249,8 @@ def block_attn(
     if softmax_scale is None:
         softmax_scale = D ** -0.5
     desc = _attn_desc(q, k_cache, v_cache, cache_seqlens, out, softmax_scale, mask_mode,
-                      mask_block, q_start, page_table, page_size, kv_split)
+                      mask_block, q_start, page_table, page_size, kv_split,
+                      0 if decode_kernel else _ffi.ATTN_NO_DECODE_KERNEL)
     L = _ffi.lib()
     need = ctypes.c_size_t(0)
     _ffi.check(L.fdllm_kv_attn_workspace_size(ctypes.byref(desc), ctypes.byref(need)),

@@ -113,7 +113,7 @@ def kv_decode_paged(seed: int = 0, batch: int = 16, num_q_heads: int = 28, num_k
     k = torch.randn(*shape, generator=g).to(dtype)
     v = torch.randn(*shape, generator=g).to(dtype)
     q = torch.randn(batch, active, num_q_heads, head_dim, generator=g).to(dtype)
-    return PagedDecode(q, k, v, table, seqlens, prefix, page_size, step % (block // active),
+    return PagedDecode(q, k, v, table, seqlens, prefix, page_size, step % max(1, block // active),
                        head_dim ** -0.5)
 
 

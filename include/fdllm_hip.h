@@ -153,14 +153,19 @@ typedef struct fdllm_kv_attn_desc {
   int32_t dtype;      /* FDLLM_DTYPE_BF16 or FDLLM_DTYPE_F16 (q, k, v, out) */
   int32_t kv_split;   /* keys per split-KV work item (multiple of 64), 0 = automatic */
   float softmax_scale;
+  int32_t flags;      /* FDLLM_ATTN_* bits, 0 = defaults */
 } fdllm_kv_attn_desc;
 
+/* Use the general kernel (one KV head per workgroup) even where the decode
+ * kernel (all KV heads of a key range per workgroup) applies. */
+#define FDLLM_ATTN_NO_DECODE_KERNEL 1
+
 /* Bytes of device workspace fdllm_kv_attn_fwd needs for `desc` (0 when the call
- * is not split over several workgroups per KV head). The first 16 KiB of the
- * workspace hold split-completion counters: zero-fill the workspace once when it
- * is allocated; every completed call leaves those counters at zero again, so one
- * workspace serves any sequence of calls of any sizes. Calls that may overlap in
- * time (different streams) need separate workspaces. */
+ * is not split over several workgroups per KV head). The workspace holds the
+ * per-split partial results (running max, sum and unnormalised output rows) that
+ * a second kernel merges; every call writes what it reads, so the contents need
+ * no initialisation and one workspace serves any sequence of calls of any sizes.
+ * Calls that may overlap in time (different streams) need separate workspaces. */
 int fdllm_kv_attn_workspace_size(const fdllm_kv_attn_desc* desc, size_t* bytes);
 
 /* Launch the attention described by `desc` on `stream`. */

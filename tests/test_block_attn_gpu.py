@@ -180,7 +180,7 @@ def test_flash_kvcache_op_and_meta(gpu):
 
 
 def test_repeated_split_calls_rearm(gpu):
-    """Split-KV completion counters are re-armed: many calls in a row stay correct."""
+    """Split-KV calls in a row on one workspace give bit-identical results."""
     wl = workloads.kv_decode_paged(seed=3, batch=4, min_prefix=512, max_prefix=2048)
     q, kp, vp = wl.q.to(gpu), wl.k_pool.to(gpu), wl.v_pool.to(gpu)
     pt, sl = wl.page_table.to(gpu), wl.seqlens.to(gpu)
@@ -191,9 +191,8 @@ def test_repeated_split_calls_rearm(gpu):
 
 
 def test_workspace_reuse_across_shapes(gpu):
-    """One workspace serves consecutive split calls of different sizes: a small call
-    (few work units) followed by a large one (many units) must not read the small
-    call's partials as completion counters."""
+    """One workspace serves consecutive split calls of different sizes: a large call
+    after a small one must not merge partials the small call left behind."""
     small = workloads.kv_decode_paged(seed=4, batch=2, min_prefix=512, max_prefix=1024)
     ops.block_attn(small.q.to(gpu), small.k_pool.to(gpu), small.v_pool.to(gpu), small.seqlens.to(gpu),
                    small.scale, page_table=small.page_table.to(gpu), page_size=small.page_size, kv_split=64)
@@ -228,3 +227,36 @@ def test_bad_page_size_rejected(gpu):
     with pytest.raises(RuntimeError, match="page_size"):
         ops.block_attn(wl.q.to(gpu), wl.k_pool.to(gpu), wl.v_pool.to(gpu), wl.seqlens.to(gpu), wl.scale,
                        page_table=wl.page_table.to(gpu), page_size=48)
+
+
+@pytest.mark.parametrize("hq,hkv,q_len", [(28, 4, 8), (28, 4, 1), (8, 8, 8), (16, 2, 32), (4, 1, 64), (32, 8, 4)])
+@pytest.mark.parametrize("paged", [False, True])
+def test_decode_kernel_vs_general(gpu, hq, hkv, q_len, paged):
+    """All-heads decode kernel and the general kernel agree with the oracle (and each other)
+    across KV-head counts, rows per head up to 64, ragged lengths and split sizes."""
+    g = torch.Generator().manual_seed(hq * 100 + hkv * 10 + q_len + paged)
+    B, D = 5, 128
+    if paged:
+        wl = workloads.kv_decode_paged(seed=hq + hkv, batch=B, num_q_heads=hq, num_kv_heads=hkv,
+                                       min_prefix=32, max_prefix=1600, active=q_len, page_size=64)
+        q, kc, vc, sl, pt, ps = wl.q, wl.k_pool, wl.v_pool, wl.seqlens, wl.page_table, 64
+        exp = oa.attention_np(q.float(), kc.float(), vc.float(), sl, page_table=pt, page_size=ps)
+    else:
+        max_s = 1700
+        q = torch.randn(B, q_len, hq, D, generator=g).to(torch.bfloat16)
+        kc = torch.randn(B, max_s, hkv, D, generator=g).to(torch.bfloat16)
+        vc = torch.randn(B, max_s, hkv, D, generator=g).to(torch.bfloat16)
+        sl = torch.tensor([1700, 33, 1, 640, 1299], dtype=torch.int32)
+        pt, ps = None, 0
+        exp = oa.attention_np(q.float(), kc.float(), vc.float(), sl)
+    print(f"case decode-vs-general {hq}/{hkv} q_len={q_len} paged={paged}", flush=True)
+    args = dict(page_table=pt.to(gpu) if pt is not None else None, page_size=ps)
+    outs = []
+    for split in (0, 64, 1 << 16):
+        for dec in (True, False):
+            o = ops.block_attn(q.to(gpu), kc.to(gpu), vc.to(gpu), sl.to(gpu), kv_split=split, decode_kernel=dec,
+                               **args)
+            _check(o, exp)
+            outs.append(o.float().cpu())
+    for o in outs[1:]:
+        torch.testing.assert_close(o, outs[0], atol=2e-2, rtol=2e-2)
