@@ -292,25 +292,26 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(const ScatterArgs a) 
   if (dst < 0 || dst >= a.S) return;
   const char* src = static_cast<const char*>(a.values) + row * a.H * a.esize;
   char* c = static_cast<char*>(a.cache) + (b * a.cs_b + dst * a.cs_s) * a.esize;
-  char* u = static_cast<char*>(a.cur) + (b * a.us_b + dst * a.us_s) * a.esize;
+  // the second destination is optional (single-destination row scatter)
+  char* u = a.cur ? static_cast<char*>(a.cur) + (b * a.us_b + dst * a.us_s) * a.esize : nullptr;
   if (a.vec16) {
     const int nvec = a.H * a.esize / 16;
     for (int i = lane; i < nvec; i += kWave) {
       const u32x4 v = reinterpret_cast<const u32x4*>(src)[i];
       reinterpret_cast<u32x4*>(c)[i] = v;
-      reinterpret_cast<u32x4*>(u)[i] = v;
+      if (u) reinterpret_cast<u32x4*>(u)[i] = v;
     }
   } else if (a.esize == 4) {
     for (int i = lane; i < a.H; i += kWave) {
       const uint32_t v = reinterpret_cast<const uint32_t*>(src)[i];
       reinterpret_cast<uint32_t*>(c)[i] = v;
-      reinterpret_cast<uint32_t*>(u)[i] = v;
+      if (u) reinterpret_cast<uint32_t*>(u)[i] = v;
     }
   } else {
     for (int i = lane; i < a.H; i += kWave) {
       const uint16_t v = reinterpret_cast<const uint16_t*>(src)[i];
       reinterpret_cast<uint16_t*>(c)[i] = v;
-      reinterpret_cast<uint16_t*>(u)[i] = v;
+      if (u) reinterpret_cast<uint16_t*>(u)[i] = v;
     }
   }
 }
@@ -466,7 +467,7 @@ extern "C" int fdllm_scatter_rows(const void* values, const int64_t* indices, in
   FDLLM_CHECK_ARG(batch >= 0 && seq_len >= 0 && num_tokens >= 0 && hidden_size > 0,
                   "fdllm_scatter_rows: bad sizes B=%d S=%d T=%d H=%d", batch, seq_len, num_tokens, hidden_size);
   if (static_cast<int64_t>(batch) * num_tokens == 0) return FDLLM_OK;
-  FDLLM_CHECK_ARG(values && indices && cache && current, "fdllm_scatter_rows: null pointer");
+  FDLLM_CHECK_ARG(values && indices && cache, "fdllm_scatter_rows: null pointer");
   ScatterArgs a;
   a.values = values;
   a.idx = indices;
@@ -483,7 +484,7 @@ extern "C" int fdllm_scatter_rows(const void* values, const int64_t* indices, in
   a.H = hidden_size;
   a.esize = es;
   a.vec16 = ((static_cast<int64_t>(hidden_size) * es) % 16 == 0) && aligned16(values) && aligned16(cache) &&
-            aligned16(current) && (cache_batch_stride * es) % 16 == 0 && (cache_row_stride * es) % 16 == 0 &&
+            (current == nullptr || aligned16(current)) && (cache_batch_stride * es) % 16 == 0 && (cache_row_stride * es) % 16 == 0 &&
             (current_batch_stride * es) % 16 == 0 && (current_row_stride * es) % 16 == 0;
   const int64_t rows = static_cast<int64_t>(batch) * num_tokens;
   scatter_rows_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,

@@ -121,17 +121,23 @@ def gather_rmsnorm(
 
 
 def scatter_rows(values: torch.Tensor, indices: torch.Tensor,
-                 cache: torch.Tensor, current: torch.Tensor) -> torch.Tensor:
-    """cache[b, indices[b,t]] = current[b, indices[b,t]] = values[b, t]; returns ``current``."""
-    if values.dim() != 3 or cache.dim() != 3 or current.dim() != 3 or indices.dim() != 2:
+                 cache: torch.Tensor, current: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
+    """cache[b, indices[b,t]] = values[b, t] (and current[b, indices[b,t]] when given).
+
+    Returns ``current`` (None when it is not given)."""
+    dests = [cache] + ([current] if current is not None else [])
+    if values.dim() != 3 or indices.dim() != 2 or any(d.dim() != 3 for d in dests):
         raise RuntimeError("scatter_rows: expected values/cache/current [B,*,H] and indices [B,T]")
-    dev = _require_gpu(values, indices, cache, current)
-    if cache.dtype != values.dtype or current.dtype != values.dtype:
+    dev = _require_gpu(values, indices, *dests)
+    if any(d.dtype != values.dtype for d in dests):
         raise RuntimeError("scatter_rows: values, cache and current must share a dtype")
-    if cache.shape != current.shape or cache.shape[0] != values.shape[0] or cache.shape[2] != values.shape[2]:
+    if cache.shape[0] != values.shape[0] or cache.shape[2] != values.shape[2] or \
+            (current is not None and current.shape != cache.shape):
         raise RuntimeError("scatter_rows: shape mismatch")
-    if cache.stride(-1) != 1 or current.stride(-1) != 1:
+    if any(d.stride(-1) != 1 for d in dests):
         raise RuntimeError("scatter_rows: cache/current last dim must be contiguous (written in place)")
+    if indices.shape[0] != values.shape[0] or indices.shape[1] != values.shape[1]:
+        raise RuntimeError("scatter_rows: indices must be [B, T] for values [B, T, H]")
     values = values.contiguous()
     if indices.dtype != torch.int64 or indices.stride(-1) != 1:
         indices = indices.to(torch.int64).contiguous()
@@ -140,7 +146,8 @@ def scatter_rows(values: torch.Tensor, indices: torch.Tensor,
     rc = _ffi.lib().fdllm_scatter_rows(
         values.data_ptr(), indices.data_ptr(), indices.stride(0),
         cache.data_ptr(), cache.stride(0), cache.stride(1),
-        current.data_ptr(), current.stride(0), current.stride(1),
+        _ptr(current), current.stride(0) if current is not None else 0,
+        current.stride(1) if current is not None else 0,
         B, S, T, H, _ffi.dtype_code(values.dtype), _ffi.stream_ptr(dev))
     _ffi.check(rc, "fdllm_scatter_rows")
     return current

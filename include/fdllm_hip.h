@@ -105,8 +105,10 @@ int fdllm_gather_rmsnorm(const void* hidden, int64_t hidden_batch_stride, int64_
  *     cache[b, s, :] = current[b, s, :] = values[b, t, :]
  *
  * values is contiguous [batch, num_tokens, hidden_size]; cache and current are
- * [batch, seq_len, hidden_size] with the given strides. Out-of-range indices
- * are skipped. Duplicate indices within a row race, as in the reference.
+ * [batch, seq_len, hidden_size] with the given strides. current may be NULL
+ * (one destination: BlockSparseCache.scatter_attn_output / scatter_mlp_output,
+ * utils/block_sparse_cache.py:112-132). Out-of-range indices are skipped.
+ * Duplicate indices within a row race, as in the reference.
  *
  * Replaces: scatter_and_return_cuda (fused_gather_norm.cu:79-119).
  * ------------------------------------------------------------------------- */

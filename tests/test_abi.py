@@ -1,0 +1,118 @@
+"""The C-ABI library: it loads on a machine without a GPU, exports every function
+that include/*.h declares, and the ctypes table binds exactly those functions.
+No kernel is launched here; argument checks that reject a call before any launch
+are exercised through the C ABI with null pointers.
+"""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADERS = sorted((ROOT / "include").glob("*.h"))
+
+
+def _declared_functions():
+    names = set()
+    for h in HEADERS:
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        text = re.sub(r"//[^\n]*", "", text)
+        for m in re.finditer(r"\b(fdllm_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from fast_v2_amd import _ffi
+    if not _ffi.LIB_PATH.exists():
+        pytest.fail(f"{_ffi.LIB_PATH} is not built (run __graft_entry__.build())")
+    return _ffi.lib()
+
+
+def test_header_declares_the_entry_points():
+    names = _declared_functions()
+    assert {"fdllm_gather_rmsnorm", "fdllm_scatter_rows", "fdllm_kv_attn_fwd",
+            "fdllm_kv_attn_workspace_size", "fdllm_kv_cache_write", "fdllm_abi_version",
+            "fdllm_last_error"} <= names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from fast_v2_amd import _ffi
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_ffi.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    missing = _declared_functions() - exported
+    assert not missing, f"declared but not exported: {sorted(missing)}"
+    for name in _declared_functions():
+        assert getattr(lib, name) is not None
+
+
+def test_ctypes_table_matches_header():
+    from fast_v2_amd import _ffi
+    assert set(_ffi.SIGNATURES) == _declared_functions()
+
+
+def test_abi_version_and_error_string(lib):
+    assert lib.fdllm_abi_version() == 1
+    assert isinstance(lib.fdllm_last_error(), bytes)
+
+
+def test_descriptor_layout_matches_c_struct():
+    """ctypes mirror of fdllm_kv_attn_desc: field order and offsets follow C layout rules."""
+    from fast_v2_amd import _ffi
+    d = _ffi.KVAttnDesc
+    assert d.q.offset == 0
+    assert d.k.offset == 32 and d.v.offset == 64 and d.out.offset == 96
+    assert d.page_table.offset == 128 and d.seqlens.offset == 136 and d.q_start.offset == 144
+    assert d.max_pages.offset == 152
+    assert d.softmax_scale.offset == d.kv_split.offset + 4
+    assert ctypes.sizeof(d) % 8 == 0
+
+
+def test_rejected_arguments_launch_nothing(lib):
+    """Calls that fail validation return a negative code and set the error text."""
+    from fast_v2_amd import _ffi
+    d = _ffi.KVAttnDesc()
+    d.dtype = _ffi.DTYPE_F32  # unsupported by the attention kernels
+    d.head_dim, d.num_q_heads, d.num_kv_heads = 128, 28, 4
+    size = ctypes.c_size_t(0)
+    rc = lib.fdllm_kv_attn_workspace_size(ctypes.byref(d), ctypes.byref(size))
+    assert rc == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    assert b"dtype" in lib.fdllm_last_error()
+    d.dtype = _ffi.DTYPE_BF16
+    d.num_q_heads = 30  # not a multiple of 4
+    assert lib.fdllm_kv_attn_workspace_size(ctypes.byref(d), ctypes.byref(size)) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    d.num_q_heads = 28
+    d.page_table = 16  # any non-null pointer: page size 48 is rejected before use
+    d.page_size, d.max_pages = 48, 4
+    assert lib.fdllm_kv_attn_workspace_size(ctypes.byref(d), ctypes.byref(size)) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    assert b"page_size" in lib.fdllm_last_error()
+    # a weighted norm mode without a weight is rejected (NULL weight only with NORM_PLAIN)
+    rc = lib.fdllm_gather_rmsnorm(None, 0, 0, None, 0, None, 0, None, None, 1, 1, 1, 64, 1e-6,
+                                  _ffi.DTYPE_BF16, _ffi.NORM_WEIGHT_AFTER_CAST, None)
+    assert rc == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    rc = lib.fdllm_kv_cache_write(None, None, 0, 0, 0, None, None, 0, 0, 0, None, 0, 0, 0, None, 0, None,
+                                  1, 1, 4, 128, _ffi.DTYPE_F32, None)
+    assert rc == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+
+
+def test_workspace_size_for_the_decode_workload(lib):
+    """The bs16 sub-block decode plan is split over several workgroups per sequence and
+    asks for a workspace; a tiny single-split call asks for none."""
+    from fast_v2_amd import _ffi
+    d = _ffi.KVAttnDesc()
+    d.dtype = _ffi.DTYPE_BF16
+    d.batch, d.q_len, d.num_q_heads, d.num_kv_heads, d.head_dim = 16, 8, 28, 4, 128
+    d.k_stride_h = d.v_stride_h = 128
+    d.max_seqlen = 4128
+    d.softmax_scale = 128 ** -0.5
+    size = ctypes.c_size_t(0)
+    assert lib.fdllm_kv_attn_workspace_size(ctypes.byref(d), ctypes.byref(size)) == 0
+    assert size.value > 0
+    d.max_seqlen = 64
+    assert lib.fdllm_kv_attn_workspace_size(ctypes.byref(d), ctypes.byref(size)) == 0
+    assert size.value == 0
