@@ -64,6 +64,7 @@ class KVAttnDesc(ctypes.Structure):
 
 
 ATTN_NO_DECODE_KERNEL = 1
+ATTN_ALL_HEADS_DECODE = 2
 
 
 # name -> (restype, argtypes); every symbol of include/fdllm_hip.h

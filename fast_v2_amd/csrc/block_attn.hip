@@ -44,6 +44,12 @@ namespace {
 constexpr int kKT = 64;        // keys per tile
 constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 (gfx9: 32-bit data format)
 constexpr int kThreads = 256;  // 4 waves
+constexpr int kSlcNt = 2;      // buffer-load cache policy: streaming (no reuse expected)
+constexpr int kMaxDecodeSplits = 16;  // key splits per (sequence, KV head) in the split decode kernel
+#ifndef FDLLM_DECODE_STAGES
+#define FDLLM_DECODE_STAGES 2
+#endif
+constexpr int kDecodeStages = FDLLM_DECODE_STAGES;  // tiles in flight per workgroup in the split decode kernel
 
 struct AttnParams {
   const uint16_t* q;
@@ -715,6 +721,353 @@ __global__ __launch_bounds__(128 * HKV) void kv_decode_kernel(const AttnParams p
   }
 }
 
+// ---------------------------------------------------------------------------
+// Split-KV decode attention, one (sequence, KV head, key range) per workgroup.
+//
+// The shape of the sub-block decode step: q_len * G <= 64 query rows share one
+// KV head, head_dim 128. Each sequence's keys are split over several workgroups
+// per KV head, which gives a grid of a few hundred workgroups whose partial
+// results are only the 64 rows of one KV head.
+//   * Workgroup = 8 waves in two teams of 4. Team tm takes the 32-key tiles
+//     t = 2j + tm of the range, so a workgroup keeps 8 waves busy (16 per CU at
+//     two workgroups per CU) without a second split of the keys; wave w of a team
+//     owns query rows 16w .. 16w + 15. The two teams' running results are merged
+//     through LDS at the end.
+//   * The key range of a sequence is cut into n = ceil(kv_end / chunk) equal
+//     splits (multiples of 32 keys), so the workgroups of one sequence do equal
+//     work; the grid is sized for the longest sequence and surplus workgroups
+//     exit at once.
+//   * Staging: each thread owns 2 K and 2 V 16-byte chunks of its team's tile,
+//     fetched NS tiles ahead into registers with buffer loads whose descriptor
+//     covers only the keys below k_hi: rows past the end read as zero without
+//     touching memory, so every step issues the same loads and the compiler's
+//     waits stay exact. Page ids of the range are read once into LDS.
+//   * LDS is double-buffered per team (K row-major with a 16-byte row pad; V
+//     row-major with a 32-byte pad for the transposing reads), so one barrier per
+//     step orders both the stores of tile t and the reads of tile t - 2.
+//   * Math as in kv_decode_kernel, one 16-row M-tile per wave: S^T = K Q^T with
+//     v_mfma_f32_16x16x32_bf16, online softmax with a lazily moved reference max,
+//     O^T += V^T P^T with the V^T operand from ds_read_b64_tr_b16.
+//   * A single-split unit writes its output rows; otherwise the unnormalised
+//     partial (O, m, l) goes to the workspace for kv_split_combine_kernel.
+template <int NS, bool F16, bool PAGED>
+__global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParams p) {
+  constexpr int D = 128;
+  constexpr int KT = 32;
+  constexpr int KS = D + 8;
+  constexpr int VS = D + 16;
+  constexpr int NDT = D / 16;
+  constexpr int kMaxPages = 160;
+  constexpr int KBUF = KT * KS;
+  constexpr int VBUF = KT * VS;
+  // [team][buffer] K then V tiles; reused for the team merge at the end
+  __shared__ __attribute__((aligned(16))) uint16_t sKV[2][2][KBUF + VBUF];
+  __shared__ int sPage[kMaxPages];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  // wave-uniform by construction; readfirstlane lets the compiler keep the
+  // per-team buffer descriptors in scalar registers
+  const int team = __builtin_amdgcn_readfirstlane(wave >> 2);
+  const int wt = wave & 3;
+  const int ttid = tid & 255;  // thread index within the team
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int b = blockIdx.z;
+  const SeqInfo si = seq_info<PAGED>(p, b, 0);
+  const int nsplit = max(1, (si.kv_end + p.chunk - 1) / p.chunk);
+  const int size = ((si.kv_end + nsplit - 1) / nsplit + KT - 1) / KT * KT;
+  const int n_act = size > 0 ? (si.kv_end + size - 1) / size : 0;
+  if (split >= max(n_act, 1)) return;
+  const int k_lo = split * size;
+  const int k_hi = min(si.kv_end, k_lo + size);
+  const int ntiles = k_hi > k_lo ? (k_hi - k_lo + KT - 1) / KT : 0;
+  const int nsteps = (ntiles + 1) / 2;  // tiles per team, rounded up (both teams run every step)
+
+  // ---- query fragments and row limits of this wave's 16 rows
+  u32x4 qf[4];
+  int lim;
+  {
+    const int r = wt * 16 + l16;
+    const int rc = min(r, p.R - 1);  // padding rows reuse a valid row: finite, never written
+    const int t = rc / p.G;
+    const int hh = rc - t * p.G;
+    lim = min(row_key_limit(p, si.seqlen, si.qs, t), k_hi);
+    const uint16_t* qrow = p.q + b * p.q_sb + t * p.q_ss + (kvh * p.G + hh) * p.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 32 + g * 8);
+  }
+  const int lim_min =
+      __builtin_amdgcn_readfirstlane(-static_cast<int>(wave_allreduce_max(-static_cast<float>(lim))));
+  const float rescale_thr = 8.f / p.scale_log2;
+
+  if constexpr (PAGED) {
+    const int32_t* pt_row = p.page_table + static_cast<int64_t>(b) * p.max_pages;
+    for (int i = tid; i < ntiles; i += 512) sPage[i] = pt_row[(k_lo + i * KT) >> p.page_shift];
+  }
+
+  f32x4 acc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // chunk c = ttid + 256 i of a tile: key c / 16, 16-byte column c % 16
+  const int krow_bytes = static_cast<int>(p.k_ss) * 2;
+  const int vrow_bytes = static_cast<int>(p.v_ss) * 2;
+  int koff[2], voff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = ttid + 256 * i;
+    koff[i] = (c >> 4) * krow_bytes + (c & 15) * 16;
+    voff[i] = (c >> 4) * vrow_bytes + (c & 15) * 16;
+  }
+  // per-workgroup bases: the KV head of this unit, sequence b (static cache)
+  const uint16_t* kbase = p.k + kvh * p.k_sh + (PAGED ? 0 : b * p.k_sp);
+  const uint16_t* vbase = p.v + kvh * p.v_sh + (PAGED ? 0 : b * p.v_sp);
+  struct Stage {
+    u32x4 k[2];
+    u32x4 v[2];
+  };
+  static_assert(NS == 2, "two register stages (named, so both paths into the loop agree on registers)");
+  Stage st0, st1;
+
+  if constexpr (PAGED) __syncthreads();  // sPage visible
+
+  // tile j of this team = tile 2j + team of the range
+  auto load_tile = [&](Stage& sg, int j) {
+    const int t = 2 * j + team;
+    const int kb = k_lo + t * KT;
+    const int valid = __builtin_amdgcn_readfirstlane(max(0, min(KT, k_hi - kb)));
+    int64_t koffs, voffs;
+    if constexpr (PAGED) {
+      const int page = __builtin_amdgcn_readfirstlane(sPage[min(t, max(ntiles - 1, 0))]);
+      const int slot0 = kb & (p.page_size - 1);
+      koffs = static_cast<int64_t>(page) * p.k_sp + slot0 * p.k_ss;
+      voffs = static_cast<int64_t>(page) * p.v_sp + slot0 * p.v_ss;
+    } else {
+      koffs = static_cast<int64_t>(kb) * p.k_ss;
+      voffs = static_cast<int64_t>(kb) * p.v_ss;
+    }
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase + koffs), 0, valid * krow_bytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase + voffs), 0, valid * vrow_bytes, kBufferFlags);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      sg.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, kSlcNt));
+      sg.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, kSlcNt));
+    }
+  };
+  auto store_tile = [&](const Stage& sg, int buf) {
+    uint16_t* sk = sKV[team][buf];
+    uint16_t* sv = sk + KBUF;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = ttid + 256 * i;
+      *reinterpret_cast<u32x4*>(&sk[(c >> 4) * KS + (c & 15) * 8]) = sg.k[i];
+      *reinterpret_cast<u32x4*>(&sv[(c >> 4) * VS + (c & 15) * 8]) = sg.v[i];
+    }
+  };
+  auto compute_tile = [&](int buf, int kb) {
+    const uint16_t* sk = sKV[team][buf];
+    const uint16_t* sv = sk + KBUF;
+    f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int st2 = 0; st2 < 2; ++st2) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(&sk[(st2 * 16 + l16) * KS + ks * 32 + g * 8]);
+        s[st2] = mfma16x16x32<F16>(kf, qf[ks], s[st2]);
+      }
+    if (!(kb + KT <= lim_min)) {  // wave-uniform: some row of the wave sees only part of the tile
+#pragma unroll
+      for (int st2 = 0; st2 < 2; ++st2)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (kb + st2 * 16 + g * 4 + j >= lim) s[st2][j] = -INFINITY;
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int st2 = 0; st2 < 2; ++st2)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, s[st2][j]);
+    tmax = group4_allreduce_max(tmax);
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + rescale_thr) != 0) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_run == -INFINITY ? 0.f : fast_exp2((m_run - m_new) * p.scale_log2);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = m_run == -INFINITY ? 0.f : m_run * p.scale_log2;
+    float lsum = 0.f;
+#pragma unroll
+    for (int st2 = 0; st2 < 2; ++st2)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float e = fast_exp2(fmaf(s[st2][j], p.scale_log2, -mc));
+        s[st2][j] = e;
+        lsum += e;
+      }
+    l_run += lsum;
+    u32x4 pf;
+    pf[0] = pack2<F16>(s[0][0], s[0][1]);
+    pf[1] = pack2<F16>(s[0][2], s[0][3]);
+    pf[2] = pack2<F16>(s[1][0], s[1][1]);
+    pf[3] = pack2<F16>(s[1][2], s[1][3]);
+    const int vrow = 4 * g + (l16 >> 2);
+    const int vcol = 4 * (l16 & 3);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const s16x4 lo = lds_read_tr16(&sv[vrow * VS + vcol + dt * 16]);
+      const s16x4 hi = lds_read_tr16(&sv[(vrow + 16) * VS + vcol + dt * 16]);
+      const u32x2 lo2 = __builtin_bit_cast(u32x2, lo);
+      const u32x2 hi2 = __builtin_bit_cast(u32x2, hi);
+      acc[dt] = mfma16x16x32<F16>(u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}, pf, acc[dt]);
+    }
+  };
+
+  // Every step stores, synchronises and issues its loads, whether or not its
+  // tile exists (loads past the range are zero-filled without memory traffic),
+  // so the number of loads in flight is the same on every path and each wait
+  // covers exactly the stage it needs; only the math is conditional.
+  auto step = [&](Stage& sg, int j) {
+    store_tile(sg, j & 1);
+    lds_barrier();
+    load_tile(sg, j + 2);
+    const int t = 2 * j + team;
+    if (t < ntiles) compute_tile(j & 1, k_lo + t * KT);  // wave-uniform
+  };
+  if (nsteps > 0) {
+    load_tile(st0, 0);
+    load_tile(st1, 1);
+    for (int j = 0; j < nsteps; j += 2) {
+      step(st0, j);
+      step(st1, j + 1);
+    }
+  }
+
+  // ---- merge the two teams: team 1 hands (m, l, O) to team 0 through LDS
+  float* xfer = reinterpret_cast<float*>(&sKV[0][0][0]);  // [4 waves][64 lanes][NDT * 4 + 2]
+  constexpr int XS = NDT * 4 + 2;
+  lds_barrier();  // every wave is done with the tiles
+  if (team == 1) {
+    float* x = xfer + (wt * 64 + lane) * XS;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) x[dt * 4 + j] = acc[dt][j];
+    x[NDT * 4] = m_run;
+    x[NDT * 4 + 1] = l_run;
+  }
+  lds_barrier();
+  if (team == 1) return;
+  {
+    const float* x = xfer + (wt * 64 + lane) * XS;
+    const float m1 = x[NDT * 4];
+    const float l1 = x[NDT * 4 + 1];
+    const float m_new = fmaxf(m_run, m1);
+    const float a0 = m_run == -INFINITY ? 0.f : fast_exp2((m_run - m_new) * p.scale_log2);
+    const float a1 = m1 == -INFINITY ? 0.f : fast_exp2((m1 - m_new) * p.scale_log2);
+    l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[dt][j] = acc[dt][j] * a0 + x[dt * 4 + j] * a1;
+    m_run = m_new;
+  }
+
+  // ---- epilogue (team 0)
+  l_run = group4_allreduce_sum(l_run);
+  const int r = wt * 16 + l16;
+  if (n_act <= 1) {
+    if (r < p.R) {
+      const int t = r / p.G;
+      const int hh = r - t * p.G;
+      const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+      uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const f32x4 o = acc[dt] * inv;
+        *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) = u32x2{pack2<F16>(o[0], o[1]), pack2<F16>(o[2], o[3])};
+      }
+    }
+    return;
+  }
+  if (r >= p.R) return;  // padding rows are never read
+  const int64_t slot = static_cast<int64_t>(b * p.Hkv + kvh) * p.n_splits + split;
+  float* po = p.ws_o + (slot * 64 + r) * D;
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16 + g * 4) = acc[dt];
+  if (g == 0) p.ws_ml[slot * 64 + r] = make_float2(m_run, l_run);
+}
+
+// Merge of kv_split_decode_kernel's partials: one thread per (row, 8 columns);
+// every split's (m, l) and partial row are loaded before any is used, so the
+// merge costs one memory round trip.
+template <bool F16, bool PAGED>
+__global__ __launch_bounds__(256) void kv_split_combine_kernel(const AttnParams p) {
+  constexpr int D = 128;
+  constexpr int MAXS = kMaxDecodeSplits;
+  const int unit = blockIdx.y;  // b * Hkv + kvh
+  const int b = unit / p.Hkv;
+  const int kvh = unit - b * p.Hkv;
+  const int r = blockIdx.x * 16 + (threadIdx.x >> 4);
+  if (r >= p.R) return;
+  const SeqInfo si = seq_info<PAGED>(p, b, 0);
+  const int nsplit = max(1, (si.kv_end + p.chunk - 1) / p.chunk);
+  const int size = ((si.kv_end + nsplit - 1) / nsplit + 31) / 32 * 32;
+  const int n_act = size > 0 ? (si.kv_end + size - 1) / size : 0;
+  if (n_act <= 1) return;  // written by the attention kernel
+  const int d0 = (threadIdx.x & 15) * 8;
+  const int64_t base = static_cast<int64_t>(unit) * p.n_splits * 64 + r;
+  float2 ml[MAXS];
+  f32x4 x0[MAXS], x1[MAXS];
+#pragma unroll
+  for (int s = 0; s < MAXS; ++s) {
+    if (s < n_act) {
+      const int64_t sl = base + static_cast<int64_t>(s) * 64;
+      ml[s] = p.ws_ml[sl];
+      const f32x4* po = reinterpret_cast<const f32x4*>(p.ws_o + sl * D + d0);
+      x0[s] = po[0];
+      x1[s] = po[1];
+    }
+  }
+  float m = -INFINITY;
+#pragma unroll
+  for (int s = 0; s < MAXS; ++s)
+    if (s < n_act) m = fmaxf(m, ml[s].x);
+  float l = 0.f;
+  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (m != -INFINITY) {
+#pragma unroll
+    for (int s = 0; s < MAXS; ++s) {
+      if (s < n_act) {
+        const float w = ml[s].x == -INFINITY ? 0.f : fast_exp2((ml[s].x - m) * p.scale_log2);
+        l += w * ml[s].y;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          o[j] += w * x0[s][j];
+          o[4 + j] += w * x1[s][j];
+        }
+      }
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  const int t = r / p.G;
+  const int hh = r - t * p.G;
+  uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh + d0;
+  u32x4 w4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) w4[j] = pack2<F16>(o[2 * j] * inv, o[2 * j + 1] * inv);
+  *reinterpret_cast<u32x4*>(orow) = w4;
+}
+
 // Merge the split partials of every (sequence, KV head, row block) with more than
 // one active split. 8 output columns per thread, D / 8 threads per row.
 template <int D, bool F16, bool PAGED>
@@ -833,11 +1186,20 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // Workspace layout: the (m, l) pairs of every split partial, then the partial
 // rows. Nothing needs to be zero: each call writes every slot it later reads.
+enum PlanKind { kPlanGeneral = 0, kPlanAllHeads = 1, kPlanSplitDecode = 2 };
+
 struct Plan {
+  int kind;     // PlanKind
   bool decode;  // all-heads decode kernel (kv_decode_kernel)
   int MT, rows_per_wg, n_rb, n_splits, chunk, R;
   size_t ws_o_bytes, ws_ml_bytes;
 };
+
+// Split-KV decode plan: keys per workgroup such that sequences of the longest
+// length would give about kSplitTargetWG workgroups (two per CU), within
+// [128, kMaxDecodeSplits splits of the longest sequence].
+constexpr int kSplitTargetWG = 448;
+constexpr int kSplitMaxChunk = 5120;  // 160 page ids of 32-key tiles in LDS
 
 int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
   FDLLM_CHECK_ARG(d != nullptr, "fdllm_kv_attn: null descriptor");
@@ -867,10 +1229,49 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
   FDLLM_CHECK_ARG(R64 < (1 << 30), "fdllm_kv_attn: q_len * group too large");
   pl->R = static_cast<int>(R64);
   const int hkv = d->num_kv_heads;
-  pl->decode = !(d->flags & FDLLM_ATTN_NO_DECODE_KERNEL) && d->head_dim == 128 && pl->R <= 64 &&
-               (hkv == 1 || hkv == 2 || hkv == 4 || hkv == 8) && d->k_stride_h == 128 && d->v_stride_h == 128 &&
-               (d->page_table == nullptr || d->page_size >= 32);
+  const bool decode_shape = !(d->flags & FDLLM_ATTN_NO_DECODE_KERNEL) && d->head_dim == 128 && pl->R <= 64 &&
+                            (d->page_table == nullptr || d->page_size >= 32) &&
+                            d->k_stride_slot >= d->head_dim && d->v_stride_slot >= d->head_dim &&
+                            d->k_stride_slot < (1 << 24) && d->v_stride_slot < (1 << 24);
+  pl->kind = kPlanGeneral;
+  if (decode_shape && !(d->flags & FDLLM_ATTN_ALL_HEADS_DECODE)) {
+    const int max_len = d->page_table
+                            ? std::min<int64_t>(d->max_seqlen, static_cast<int64_t>(d->max_pages) * d->page_size)
+                            : d->max_seqlen;
+    const int64_t len = std::max(1, max_len);
+    int64_t chunk;
+    if (d->kv_split > 0) {
+      chunk = d->kv_split;
+    } else {
+      const int64_t total = static_cast<int64_t>(std::max(d->batch, 1)) * d->num_kv_heads * len;
+      chunk = (total + kSplitTargetWG - 1) / kSplitTargetWG;
+      chunk = std::max<int64_t>(chunk, 128);
+    }
+    chunk = std::max<int64_t>(chunk, (len + kMaxDecodeSplits - 1) / kMaxDecodeSplits);
+    chunk = (chunk + 31) / 32 * 32;
+    chunk = std::min<int64_t>(chunk, (len + 31) / 32 * 32);
+    if (chunk <= kSplitMaxChunk) {
+      pl->kind = kPlanSplitDecode;
+      pl->decode = false;
+      pl->MT = 1;
+      pl->rows_per_wg = 64;
+      pl->n_rb = 1;
+      pl->chunk = static_cast<int>(chunk);
+      pl->n_splits = static_cast<int>((len + chunk - 1) / chunk);
+      const int64_t units = static_cast<int64_t>(d->batch) * hkv;
+      if (pl->n_splits > 1) {
+        pl->ws_o_bytes = static_cast<size_t>(units) * pl->n_splits * 64 * d->head_dim * sizeof(float);
+        pl->ws_ml_bytes = static_cast<size_t>(units) * pl->n_splits * 64 * sizeof(float2);
+      } else {
+        pl->ws_o_bytes = pl->ws_ml_bytes = 0;
+      }
+      return FDLLM_OK;
+    }
+  }
+  pl->decode = decode_shape && (hkv == 1 || hkv == 2 || hkv == 4 || hkv == 8) && d->k_stride_h == 128 &&
+               d->v_stride_h == 128;
   if (pl->decode) {
+    pl->kind = kPlanAllHeads;
     const int max_len = d->page_table
                             ? std::min<int64_t>(d->max_seqlen, static_cast<int64_t>(d->max_pages) * d->page_size)
                             : d->max_seqlen;
@@ -1075,6 +1476,28 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
   }
   const bool f16 = d->dtype == FDLLM_DTYPE_F16;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.kind == kPlanSplitDecode) {
+    const bool paged = p.page_table != nullptr;
+    const dim3 grid(pl.n_splits, d->num_kv_heads, d->batch);
+    if (f16) {
+      if (paged) kv_split_decode_kernel<kDecodeStages, true, true><<<grid, dim3(512), 0, s>>>(p);
+      else kv_split_decode_kernel<kDecodeStages, true, false><<<grid, dim3(512), 0, s>>>(p);
+    } else {
+      if (paged) kv_split_decode_kernel<kDecodeStages, false, true><<<grid, dim3(512), 0, s>>>(p);
+      else kv_split_decode_kernel<kDecodeStages, false, false><<<grid, dim3(512), 0, s>>>(p);
+    }
+    if (pl.n_splits > 1) {
+      const dim3 cgrid((pl.R + 15) / 16, static_cast<unsigned>(grid_z));
+      if (f16) {
+        if (paged) kv_split_combine_kernel<true, true><<<cgrid, dim3(256), 0, s>>>(p);
+        else kv_split_combine_kernel<true, false><<<cgrid, dim3(256), 0, s>>>(p);
+      } else {
+        if (paged) kv_split_combine_kernel<false, true><<<cgrid, dim3(256), 0, s>>>(p);
+        else kv_split_combine_kernel<false, false><<<cgrid, dim3(256), 0, s>>>(p);
+      }
+    }
+    FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
+  }
   if (pl.decode) {
     switch (d->num_kv_heads) {
       case 1: launch_decode<1>(p, f16, s); break;

@@ -205,6 +205,7 @@ def block_attn(
     out: Optional[torch.Tensor] = None,
     kv_split: int = 0,
     decode_kernel: bool = True,
+    all_heads_decode: bool = False,
 ) -> torch.Tensor:
     """Attention of BSHD queries over a (paged) BSHD KV cache.
 
@@ -213,8 +214,9 @@ def block_attn(
                  [num_pages, page_size, Hkv, D] with ``page_table`` [B, max_pages] int32
     cache_seqlens [B] visible key count per sequence (int32; other ints converted)
     Returns a new [B, Sq, Hq, D] tensor (or fills ``out``).
-    decode_kernel=False forces the general kernel where the all-heads decode
-    kernel would apply (both compute the same function).
+    decode_kernel=False forces the general kernel where a decode kernel would
+    apply; all_heads_decode=True picks the all-KV-heads decode kernel instead of
+    the split-KV one (all compute the same function).
     """
     if q.dim() != 4 or k_cache.dim() != 4 or v_cache.dim() != 4:
         raise RuntimeError("block_attn: q, k_cache and v_cache must be 4-D (BSHD)")
@@ -257,7 +259,8 @@ def block_attn(
         softmax_scale = D ** -0.5
     desc = _attn_desc(q, k_cache, v_cache, cache_seqlens, out, softmax_scale, mask_mode,
                       mask_block, q_start, page_table, page_size, kv_split,
-                      0 if decode_kernel else _ffi.ATTN_NO_DECODE_KERNEL)
+                      (0 if decode_kernel else _ffi.ATTN_NO_DECODE_KERNEL)
+                      | (_ffi.ATTN_ALL_HEADS_DECODE if all_heads_decode else 0))
     L = _ffi.lib()
     need = ctypes.c_size_t(0)
     _ffi.check(L.fdllm_kv_attn_workspace_size(ctypes.byref(desc), ctypes.byref(need)),

@@ -161,6 +161,9 @@ typedef struct fdllm_kv_attn_desc {
 /* Use the general kernel (one KV head per workgroup) even where the decode
  * kernel (all KV heads of a key range per workgroup) applies. */
 #define FDLLM_ATTN_NO_DECODE_KERNEL 1
+/* Decode shapes: use the all-KV-heads-per-workgroup kernel instead of the
+ * split-KV kernel with one KV head per workgroup. */
+#define FDLLM_ATTN_ALL_HEADS_DECODE 2
 
 /* Bytes of device workspace fdllm_kv_attn_fwd needs for `desc` (0 when the call
  * is not split over several workgroups per KV head). The workspace holds the

@@ -232,8 +232,9 @@ def test_bad_page_size_rejected(gpu):
 @pytest.mark.parametrize("hq,hkv,q_len", [(28, 4, 8), (28, 4, 1), (8, 8, 8), (16, 2, 32), (4, 1, 64), (32, 8, 4)])
 @pytest.mark.parametrize("paged", [False, True])
 def test_decode_kernel_vs_general(gpu, hq, hkv, q_len, paged):
-    """All-heads decode kernel and the general kernel agree with the oracle (and each other)
-    across KV-head counts, rows per head up to 64, ragged lengths and split sizes."""
+    """Split-KV decode kernel, all-heads decode kernel and the general kernel agree with the
+    oracle (and each other) across KV-head counts, rows per head up to 64, ragged lengths
+    and split sizes."""
     g = torch.Generator().manual_seed(hq * 100 + hkv * 10 + q_len + paged)
     B, D = 5, 128
     if paged:
@@ -253,9 +254,9 @@ def test_decode_kernel_vs_general(gpu, hq, hkv, q_len, paged):
     args = dict(page_table=pt.to(gpu) if pt is not None else None, page_size=ps)
     outs = []
     for split in (0, 64, 1 << 16):
-        for dec in (True, False):
+        for dec, allh in ((True, False), (True, True), (False, False)):
             o = ops.block_attn(q.to(gpu), kc.to(gpu), vc.to(gpu), sl.to(gpu), kv_split=split, decode_kernel=dec,
-                               **args)
+                               all_heads_decode=allh, **args)
             _check(o, exp)
             outs.append(o.float().cpu())
     for o in outs[1:]:
