@@ -1196,9 +1196,9 @@ struct Plan {
 };
 
 // Split-KV decode plan: keys per workgroup such that sequences of the longest
-// length would give about kSplitTargetWG workgroups (two per CU), within
+// length would give about kSplitTargetWG workgroups (one per CU), within
 // [128, kMaxDecodeSplits splits of the longest sequence].
-constexpr int kSplitTargetWG = 448;
+constexpr int kSplitTargetWG = 256;
 constexpr int kSplitMaxChunk = 5120;  // 160 page ids of 32-key tiles in LDS
 
 int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
