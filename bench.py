@@ -255,6 +255,36 @@ def bench_prefill(torch, args):
     return res
 
 
+def bench_e2e(torch, args):
+    """End-to-end block-diffusion generation with the random-init 7B-layout model on the
+    HIP path: batch 16, 512-token prompts, ``--e2e-tokens`` new tokens, 32-token blocks,
+    8-token sub-blocks, threshold 0.9, block cache on. tokens/s = generated tokens /
+    generation wall time (eval.py:425-429); one short untimed run first."""
+    from fast_v2_amd.e2e import model as em
+    from fast_v2_amd.e2e import sampler as es
+
+    dev = torch.device("cuda", 0)
+    cfg = em.BlockDiffusionConfig()
+    t0 = time.perf_counter()
+    model = em.build_model(cfg, dev)
+    torch.cuda.synchronize()
+    build_s = time.perf_counter() - t0
+    g = torch.Generator().manual_seed(0)
+    x = torch.randint(0, cfg.vocab_size - 1, (16, 512), generator=g).to(dev)
+    es.generate(model, x, max_new_tokens=64, use_block_cache=True)  # warm-up
+    out, st = es.generate(model, x, max_new_tokens=args.e2e_tokens, use_block_cache=True)
+    res = {"tokens_per_s": round(st.tokens_per_second, 1), "generated_tokens": st.generated_tokens,
+           "seconds": round(st.seconds, 3), "forwards": st.forwards, "commits": st.commits,
+           "ms_per_forward": round(st.seconds * 1e3 / max(st.forwards, 1), 3),
+           "tokens_per_step": round(sum(st.step_tokens) / max(len(st.step_tokens), 1), 3),
+           "params": em.param_count(cfg), "model_build_s": round(build_s, 2),
+           "config": "28 layers, hidden 3584, 28/4 heads, vocab 152064, bf16 random init; batch 16, prompt 512, "
+                     f"{args.e2e_tokens} new tokens, block 32, sub-block 8, threshold 0.9 (p > 0.9), block cache on"}
+    del model, out, x
+    torch.cuda.empty_cache()
+    return res
+
+
 def calibrate_copies(torch):
     """Plain torch device copies (read N + write N bytes) timed the same way as the
     kernels: the practical bandwidth of a kernel of that size, launch gap included."""
@@ -290,7 +320,9 @@ def main() -> int:
     ap.add_argument("--no-check", action="store_true", help="skip the graph-vs-eager equality check")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["decode", "gather", "prefill"], default=None)
+    ap.add_argument("--only", choices=["decode", "gather", "prefill", "e2e"], default=None)
+    ap.add_argument("--e2e-tokens", type=int, default=1024, help="tokens generated in the end-to-end leg")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end generation leg")
     ap.add_argument("--calibrate", action="store_true",
                     help="also time plain device copies of the workloads' sizes (practical bandwidth floor)")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -336,6 +368,11 @@ def main() -> int:
         extra["prefill"] = bench_prefill(torch, args)
         _log(f"prefill: {extra['prefill']['us_attention_kernel']:.1f} us attention, "
              f"{extra['prefill']['roofline']['achieved']:.0f} TFLOP/s")
+
+    if args.only == "e2e" or (args.only is None and not args.no_e2e):
+        extra["e2e"] = bench_e2e(torch, args)
+        _log(f"e2e: {extra['e2e']['tokens_per_s']} tokens/s ({extra['e2e']['forwards']} forwards, "
+             f"{extra['e2e']['seconds']} s)")
 
     cpu = None
     if decode is not None and not args.no_cpu_baseline:

@@ -1,0 +1,196 @@
+"""Qwen2.5-layout block-diffusion LM (the Fast-dLLM v2 7B architecture) for the
+end-to-end generation workload, with random weights (no checkpoint is available).
+
+Layout follows the reference model (models/.../modeling.py): RMSNorm with the
+Fast_dLLM_QwenRMSNorm rounding order (:427-432), q/k/v projections with bias and
+o_proj without (:314-325), SiLU-gated MLP (:153-166), RoPE with theta 1e6
+computed in fp32 and cast to the activation dtype (:544-556), weights initialised
+as in _init_weights (:511-522): Linear / Embedding ~ N(0, 0.02), biases 0, norm
+weights 1.
+
+The attention modules carry the attributes the layer patching of
+utils/attention_backends.py reads (layer_idx, head_dim, scaling, q/k/v/o_proj);
+their own forward refuses to run, so the model is used with
+``patch_attention_layers`` as batch_sample_dynamo does
+(generation_functions.py:382-385).
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+@dataclass
+class BlockDiffusionConfig:
+    vocab_size: int = 152064
+    hidden_size: int = 3584
+    intermediate_size: int = 18944
+    num_hidden_layers: int = 28
+    num_attention_heads: int = 28
+    num_key_value_heads: int = 4
+    rms_norm_eps: float = 1e-6
+    rope_theta: float = 1_000_000.0
+    initializer_range: float = 0.02
+    bd_size: int = 32
+
+    @property
+    def head_dim(self) -> int:
+        return self.hidden_size // self.num_attention_heads
+
+
+class RMSNorm(nn.Module):
+    """w * (x.f32 * rsqrt(mean(x.f32^2) + eps)).to(dtype) (modeling.py:427-432)."""
+
+    def __init__(self, hidden_size: int, eps: float):
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(hidden_size))
+        self.variance_epsilon = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        dt = x.dtype
+        h = x.float()
+        h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + self.variance_epsilon)
+        return self.weight * h.to(dt)
+
+
+class Attention(nn.Module):
+    def __init__(self, cfg: BlockDiffusionConfig, layer_idx: int):
+        super().__init__()
+        self.layer_idx = layer_idx
+        self.head_dim = cfg.head_dim
+        self.scaling = self.head_dim ** -0.5
+        self.q_proj = nn.Linear(cfg.hidden_size, cfg.num_attention_heads * self.head_dim, bias=True)
+        self.k_proj = nn.Linear(cfg.hidden_size, cfg.num_key_value_heads * self.head_dim, bias=True)
+        self.v_proj = nn.Linear(cfg.hidden_size, cfg.num_key_value_heads * self.head_dim, bias=True)
+        self.o_proj = nn.Linear(cfg.num_attention_heads * self.head_dim, cfg.hidden_size, bias=False)
+
+    def forward(self, *args, **kwargs):
+        raise RuntimeError("attention layers run through patch_attention_layers "
+                           "(fast_v2_amd.utils.attention_backends)")
+
+
+class MLP(nn.Module):
+    def __init__(self, cfg: BlockDiffusionConfig):
+        super().__init__()
+        self.gate_proj = nn.Linear(cfg.hidden_size, cfg.intermediate_size, bias=False)
+        self.up_proj = nn.Linear(cfg.hidden_size, cfg.intermediate_size, bias=False)
+        self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, cfg: BlockDiffusionConfig, layer_idx: int):
+        super().__init__()
+        self.self_attn = Attention(cfg, layer_idx)
+        self.mlp = MLP(cfg)
+        self.input_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+
+    def forward(self, h, position_embeddings, past_key_value, update_past_key_values, block_past_key_values,
+                replace_position):
+        a = self.self_attn(self.input_layernorm(h), position_embeddings, None, past_key_value, None,
+                           update_past_key_values, block_past_key_values, replace_position)
+        h = h + a
+        return h + self.mlp(self.post_attention_layernorm(h))
+
+
+class Backbone(nn.Module):
+    def __init__(self, cfg: BlockDiffusionConfig):
+        super().__init__()
+        self.embed_tokens = nn.Embedding(cfg.vocab_size, cfg.hidden_size)
+        self.layers = nn.ModuleList(DecoderLayer(cfg, i) for i in range(cfg.num_hidden_layers))
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
+        d = cfg.head_dim
+        self.register_buffer("inv_freq", 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d)),
+                             persistent=False)
+
+    def rotary(self, positions: torch.Tensor, dtype: torch.dtype):
+        """cos / sin [1, S, D] for absolute positions [S] (fp32, then cast)."""
+        freqs = positions.float()[:, None] * self.inv_freq.float()[None, :]
+        emb = torch.cat((freqs, freqs), dim=-1)
+        return emb.cos().to(dtype)[None], emb.sin().to(dtype)[None]
+
+
+class BlockDiffusionLM(nn.Module):
+    """Embedding -> decoder layers -> norm -> lm_head, over a static KV cache."""
+
+    def __init__(self, cfg: BlockDiffusionConfig):
+        super().__init__()
+        self.config = cfg
+        self.model = Backbone(cfg)
+        self.lm_head = nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False)
+
+    @torch.no_grad()
+    def init_weights(self, seed: int = 0) -> None:
+        """_init_weights (modeling.py:511-522), drawn on the module's device."""
+        dev = self.lm_head.weight.device
+        gen = torch.Generator(device=dev).manual_seed(seed)
+        std = self.config.initializer_range
+        for mod in self.modules():
+            if isinstance(mod, nn.Linear):
+                mod.weight.normal_(0.0, std, generator=gen)
+                if mod.bias is not None:
+                    mod.bias.zero_()
+            elif isinstance(mod, nn.Embedding):
+                mod.weight.normal_(0.0, std, generator=gen)
+            elif isinstance(mod, RMSNorm):
+                mod.weight.fill_(1.0)
+
+    @torch.no_grad()
+    def forward(self, input_ids: torch.Tensor, past_key_values, update_past_key_values: bool = False,
+                use_block_cache: bool = False, block_past_key_values=None, replace_position: Optional[int] = None,
+                cache_position: Optional[torch.Tensor] = None, logits_to_keep: int = 0) -> torch.Tensor:
+        """Logits [B, logits_to_keep or S, vocab] for ``input_ids`` [B, S].
+
+        Positions (forward_dynamo, modeling.py:715-733): ``cache_position`` if given,
+        else the committed length (plus ``replace_position`` for a sub-block step)
+        onwards."""
+        h = self.model.embed_tokens(input_ids)
+        S = input_ids.shape[1]
+        if cache_position is None:
+            start = past_key_values.get_seq_length()
+            if use_block_cache and replace_position is not None:
+                start += int(replace_position)
+            cache_position = torch.arange(start, start + S, device=input_ids.device)
+        pe = self.model.rotary(cache_position, h.dtype)
+        bpkv = block_past_key_values if use_block_cache else None
+        for layer in self.model.layers:
+            h = layer(h, pe, past_key_values, update_past_key_values, bpkv, replace_position)
+        h = self.model.norm(h)
+        if logits_to_keep:
+            h = h[:, -logits_to_keep:]
+        return self.lm_head(h)
+
+
+def build_model(cfg: BlockDiffusionConfig, device, dtype=torch.bfloat16, seed: int = 0) -> BlockDiffusionLM:
+    """Allocate the model directly on ``device`` in ``dtype`` (no host copy, no default
+    initialisation pass) and initialise it with ``init_weights``."""
+    old = torch.get_default_dtype()
+    torch.set_default_dtype(dtype)
+    try:
+        with torch.device("meta"):
+            model = BlockDiffusionLM(cfg)
+    finally:
+        torch.set_default_dtype(old)
+    model = model.to_empty(device=device)
+    d = cfg.head_dim
+    model.model.inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32, device=device) / d))
+    model.init_weights(seed)
+    model.eval()
+    return model
+
+
+def param_count(cfg: BlockDiffusionConfig) -> int:
+    h, i, v, L = cfg.hidden_size, cfg.intermediate_size, cfg.vocab_size, cfg.num_hidden_layers
+    kv = cfg.num_key_value_heads * cfg.head_dim
+    per_layer = h * h + h + 2 * (h * kv + kv) + h * h + 3 * h * i + 2 * h
+    return v * h * 2 + L * per_layer + h
+
+
+__all__ = ["BlockDiffusionConfig", "BlockDiffusionLM", "build_model", "param_count", "RMSNorm"]

@@ -1,0 +1,196 @@
+"""Static-KV block-diffusion sampler: batch_sample_dynamo
+(generation_functions.py:243-954) in eager execution with a fixed batch.
+
+Per block of ``block_size`` tokens (generation_functions.py:586-700):
+  * the block is filled with ``mask_id`` and the cache's control signals are set
+    (kv_write_start = committed length, scratch_seqlens = committed + block);
+  * for each sub-block of ``small_block_size`` tokens, repeat until none of its
+    tokens is masked: run the model (the full block, or only the sub-block when the
+    block cache holds the block's K/V and the sub-block's first token is known,
+    :723-756), shift the logits by one position (:774), take the greedy token and
+    its probability, unmask every masked token whose probability exceeds
+    ``threshold`` (strict ``>``, :791) and at least the most probable one per row
+    (:792-794);
+  * commit: run the block once more with update_past_key_values=True, which writes
+    its K/V at the committed position and advances it, and append the argmax of the
+    last position as the first token of the next block (:685-696).
+The prompt is prefilled the same way (:557-575); on this static path the prefill
+attention sees the whole prompt (the patched forward ignores the block mask).
+
+Attention and KV caching come from an ``impl`` object, so the same loop runs on
+the HIP kernels (``HipStaticAttention``, the product) or on any other
+implementation of the same cache interface.
+"""
+from __future__ import annotations
+
+import time
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+from ..utils.attention_backends import get_attention_backend, patch_attention_layers, unpatch_attention_layers
+from ..utils.static_kv_cache import StaticBlockCache, StaticKVCache
+
+
+class HipStaticAttention:
+    """StaticKVCache / StaticBlockCache with HIP writes + the 'hip' attention backend."""
+
+    name = "hip"
+
+    def make_caches(self, batch, max_seq_len, cfg, dtype, device, use_block_cache):
+        cache = StaticKVCache(batch, max_seq_len, cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim,
+                              dtype, device)
+        block = (StaticBlockCache(batch, cfg.bd_size, cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim,
+                                  dtype, device) if use_block_cache else None)
+        return cache, block
+
+    def patch(self, model, block_cache):
+        return patch_attention_layers(model, get_attention_backend("hip"), block_cache)
+
+    def unpatch(self, model, originals):
+        unpatch_attention_layers(model, originals)
+
+
+@dataclass
+class GenerationStats:
+    forwards: int = 0
+    commits: int = 0
+    blocks: int = 0
+    seconds: float = 0.0
+    generated_tokens: int = 0
+    step_tokens: list = field(default_factory=list)
+
+    @property
+    def tokens_per_second(self) -> float:
+        return self.generated_tokens / self.seconds if self.seconds > 0 else 0.0
+
+
+def greedy_with_confidence(logits: torch.Tensor):
+    """sample_with_top_p at temperature 0 (modeling.py:2263-2270): softmax in the
+    logits' dtype, argmax token and its probability."""
+    p = torch.softmax(logits, dim=-1)
+    x = p.argmax(dim=-1)
+    return x, torch.gather(p, -1, x.unsqueeze(-1)).squeeze(-1)
+
+
+def threshold_unmask(tok: torch.Tensor, conf: torch.Tensor, masked: torch.Tensor, threshold: float):
+    """Unmask every masked position whose confidence exceeds ``threshold`` and the
+    most confident masked position of each row (generation_functions.py:784-795)."""
+    conf = torch.where(masked, conf, torch.full_like(conf, float("-inf")))
+    unmask = conf > threshold
+    unmask[torch.arange(conf.shape[0], device=conf.device), conf.argmax(dim=-1)] = True
+    return unmask & masked
+
+
+@torch.no_grad()
+def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_size: int = 32,
+             small_block_size: int = 8, mask_id: int = 152063, threshold: float = 0.9,
+             use_block_cache: bool = True, stop_token: Optional[int] = None, pad_token: int = 0,
+             impl=None, max_seq_len: Optional[int] = None, sync_timing: bool = True, policy=None,
+             bridge_policy=None):
+    """Generate for a batch of equal-length prompts [B, P]; returns (tokens [B, P + N + 1], stats).
+
+    Equal prompt lengths are the config of the end-to-end workload; the reference's
+    per-row bookkeeping for ragged prompts (BatchBucket) is not needed for it.
+    ``policy(step, tok, conf, masked) -> (tok, unmask)`` replaces the greedy threshold
+    rule when given (``step`` counts sampling steps from 0); ``bridge_policy(i, tok) ->
+    tok`` likewise replaces the argmax token that opens each block (i = 0 after the
+    prefill, then one per commit)."""
+    n_bridge = [0]
+
+    def bridge(tok):
+        if bridge_policy is not None:
+            tok = bridge_policy(n_bridge[0], tok)
+        n_bridge[0] += 1
+        return tok
+
+    impl = impl or HipStaticAttention()
+    cfg = model.config
+    B, P = input_ids.shape
+    dev = input_ids.device
+    dtype = model.lm_head.weight.dtype
+    if max_seq_len is None:
+        need = P + max_new_tokens + block_size
+        max_seq_len = (need + 255) // 256 * 256
+    cache, block_cache = impl.make_caches(B, max_seq_len, cfg, dtype, dev, use_block_cache)
+    originals = impl.patch(model, block_cache)
+    stats = GenerationStats()
+    try:
+        if sync_timing:
+            torch.cuda.synchronize(dev)
+        t0 = time.perf_counter()
+        x = input_ids.clone()
+        min_len = P
+        # ---- prefill (generation_functions.py:557-575)
+        if min_len > block_size:
+            prefill_len = min_len // block_size * block_size
+            logits = model(x[:, :prefill_len], cache, update_past_key_values=True)
+            stats.forwards += 1
+            if min_len % block_size == 0:
+                x = torch.cat([x, bridge(logits[:, -1:].argmax(dim=-1))], dim=1)
+        num_blocks = max_new_tokens // block_size + P // block_size
+        finished = torch.zeros(B, dtype=torch.bool, device=dev)
+        for block_idx in range(min_len // block_size, num_blocks):
+            if x.shape[1] < (block_idx + 1) * block_size:
+                pad_len = (block_idx + 1) * block_size - x.shape[1]
+                x = torch.cat([x, torch.full((B, pad_len), mask_id, dtype=x.dtype, device=dev)], dim=1)
+            if block_cache is not None:
+                block_cache.reset()
+            past_len = cache.get_seq_length()
+            cache.set_kv_write_start(past_len)
+            cache.set_scratch_seqlens(past_len + block_size)
+            cache.prepare_write_idx(block_size)
+            cache_pos = torch.arange(past_len, past_len + block_size, device=dev)
+            stats.blocks += 1
+            blk = slice(block_idx * block_size, (block_idx + 1) * block_size)
+            for sb in range(block_size // small_block_size):
+                s0, s1 = sb * small_block_size, (sb + 1) * small_block_size
+                while True:
+                    mask = x[:, blk] == mask_id
+                    if not bool(mask[:, s0:s1].any()):
+                        break
+                    if use_block_cache and len(block_cache) > 0 and not bool(mask[:, s0].any()):
+                        logits = model(x[:, blk][:, s0:s1], cache, use_block_cache=True,
+                                       block_past_key_values=block_cache, replace_position=s0,
+                                       logits_to_keep=small_block_size)
+                        logits = torch.cat([logits[:, :1], logits[:, :-1]], dim=1)
+                    else:
+                        logits = model(x[:, blk], cache, use_block_cache=use_block_cache,
+                                       block_past_key_values=block_cache, cache_position=cache_pos,
+                                       logits_to_keep=block_size)
+                        logits = torch.cat([logits[:, :1], logits[:, :-1]], dim=1)[:, s0:s1]
+                    stats.forwards += 1
+                    tok, conf = greedy_with_confidence(logits)
+                    m = mask[:, s0:s1] & ~finished[:, None]
+                    if policy is None:
+                        unmask = threshold_unmask(tok, conf, m, threshold)
+                    else:
+                        tok, unmask = policy(len(stats.step_tokens), tok, conf, m)
+                    sub = x[:, blk][:, s0:s1]
+                    x[:, blk.start + s0:blk.start + s1] = torch.where(unmask, tok, sub)
+                    if stop_token is not None:
+                        finished |= ((tok == stop_token) & unmask).any(dim=1)
+                    stats.step_tokens.append(int(unmask.sum()))
+                    if bool(finished.all()):
+                        break
+            # ---- commit (generation_functions.py:685-696)
+            logits = model(x[:, blk], cache, update_past_key_values=True)
+            stats.forwards += 1
+            stats.commits += 1
+            nxt = bridge(logits[:, -1:].argmax(dim=-1))
+            nxt[finished] = pad_token
+            x = torch.cat([x, nxt], dim=1)
+            if bool(finished.all()):
+                break
+        if sync_timing:
+            torch.cuda.synchronize(dev)
+        stats.seconds = time.perf_counter() - t0
+        gen = x[:, P:P + max_new_tokens]
+        stats.generated_tokens = int((gen != mask_id).sum())
+        return x, stats
+    finally:
+        impl.unpatch(model, originals)
+
+
+__all__ = ["generate", "greedy_with_confidence", "threshold_unmask", "HipStaticAttention", "GenerationStats"]

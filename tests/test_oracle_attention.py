@@ -242,3 +242,19 @@ def test_repeat_kv_map():
     assert r.shape == (2, 12, 1, 1)
     for h in range(12):
         assert torch.equal(r[:, h], x[:, h // 4])
+
+
+def test_e2e_oracle_attention_variants():
+    """The eager e2e oracle's float32 attention equals the SDPA shim; its bf16-P variant
+    differs only by the rounding of the probabilities (bounded by bf16 resolution)."""
+    from oracle.e2e_eager import kvcache_attention_f32
+    g = torch.Generator().manual_seed(9)
+    q, k, v = torch.randn(3, 5, 8, 32, generator=g), torch.randn(3, 40, 2, 32, generator=g), \
+        torch.randn(3, 40, 2, 32, generator=g)
+    sl = torch.tensor([40, 9, 1])
+    ref = oa.sdpa_kvcache(q, k, v, sl, scaling=0.2)
+    torch.testing.assert_close(kvcache_attention_f32(q, k, v, sl, 0.2, False), ref, atol=1e-5, rtol=1e-5)
+    lo = kvcache_attention_f32(q, k, v, sl, 0.2, True)
+    assert 0 < (lo - ref).abs().max() < 2e-2
+    # one visible key: p = 1 exactly in bf16, so both variants return that value row
+    torch.testing.assert_close(lo[2], v[2, 0].repeat_interleave(4, 0)[None].expand(5, 8, 32), atol=0, rtol=0)
