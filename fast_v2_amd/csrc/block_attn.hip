@@ -45,6 +45,11 @@ constexpr int kKT = 64;        // keys per tile
 constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 (gfx9: 32-bit data format)
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kSlcNt = 2;      // buffer-load cache policy: streaming (no reuse expected)
+// Buffer load/store cache policy "sc1": coherent at device scope. With 8 XCDs the L2
+// caches are per XCD; sc1 stores write through to memory and sc1 loads do not hit
+// another XCD's stale copy, which is all a cross-workgroup handoff of a few KiB needs
+// (the agent-scope fences of the HIP memory model write back and invalidate whole L2s).
+constexpr int kSc1 = 16;
 constexpr int kMaxDecodeSplits = 16;  // key splits per (sequence, KV head) in the split decode kernel
 #ifndef FDLLM_DECODE_STAGES
 #define FDLLM_DECODE_STAGES 2
@@ -68,12 +73,13 @@ struct AttnParams {
   int R;            // rows per (b, kv head) = Sq * G
   int rows_per_wg;  // 64 * MT
   int n_rb;         // row blocks per (b, kv head)
-  int n_splits;     // split slots per row block (grid x)
-  int chunk;        // keys per split, multiple of kKT
+  int n_splits;     // split slots per row block (grid x); split decode: partial slots per KV head
+  int chunk;        // keys per split, multiple of kKT; split decode: 0 = balanced partition
   int mask_mode, mask_block;
   float scale_log2;  // softmax_scale * log2(e)
   float* ws_o;       // [units, n_splits, rows_per_wg, D]
   float2* ws_ml;     // [units, n_splits, rows_per_wg]
+  int* ws_cnt;       // [units] arrival counters of the split decode kernel (zero between calls)
 };
 
 template <bool F16>
@@ -140,12 +146,14 @@ struct SeqInfo {
 template <bool PAGED>
 __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b, int rb) {
   SeqInfo si;
+  // both loads issue before either is waited for (q_start falls back to a dummy read)
   int seqlen = p.seqlens[b];
+  const int qs_raw = (p.q_start ? p.q_start : p.seqlens)[b];
   if (seqlen > p.max_seqlen) seqlen = p.max_seqlen;
   if (PAGED && seqlen > p.max_pages * p.page_size) seqlen = p.max_pages * p.page_size;
   if (seqlen < 0) seqlen = 0;
   si.seqlen = seqlen;
-  si.qs = p.q_start ? p.q_start[b] : seqlen - p.Sq;
+  si.qs = p.q_start ? qs_raw : seqlen - p.Sq;
   const int row0 = rb * p.rows_per_wg;
   const int row_last = min(p.R, row0 + p.rows_per_wg) - 1;  // limits grow with t
   si.kv_end = max(0, row_key_limit(p, seqlen, si.qs, row_last / p.G));
@@ -721,6 +729,193 @@ __global__ __launch_bounds__(128 * HKV) void kv_decode_kernel(const AttnParams p
   }
 }
 
+// Inclusive prefix sum over the 64 lanes of a wave with DPP moves: shifts by 1,
+// 2, 4 and 8 within each 16-lane row, then the running totals of rows 0 and 1
+// broadcast into the rows above them (row_bcast:15 into rows 1 and 3, row_bcast:31
+// into rows 2 and 3). Lanes whose DPP source lies outside the row add 0.
+__device__ __forceinline__ int wave_incl_scan_i32(int v) {
+  v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, false);  // row_shr:1
+  v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, false);  // row_shr:2
+  v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, false);  // row_shr:4
+  v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, false);  // row_shr:8
+  v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false);  // row_bcast:15
+  v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false);  // row_bcast:31
+  return v;
+}
+__device__ __forceinline__ int wave_sum_i32(int v) {
+  return __builtin_amdgcn_readlane(wave_incl_scan_i32(v), 63);
+}
+
+// ceil(a / b) for 0 <= a < 2^20 and 1 <= b < 2^20: the float quotient is within
+// 0.25 of a / b, its truncation at most one below floor(a / b), and two exact
+// integer corrections reach the ceiling.
+__device__ __forceinline__ int ceil_div_small(int a, int b) {
+  int q = static_cast<int>(static_cast<float>(a) * __builtin_amdgcn_rcpf(static_cast<float>(b)));
+  q += q * b < a;
+  q += q * b < a;
+  return q;
+}
+
+constexpr int kDecodeMaxTiles = 160;  // 32-key tiles per split: page ids staged in LDS
+
+// Key range of one workgroup of the split decode kernel.
+struct DecodePart {
+  int b;       // sequence, -1 for an idle workgroup
+  int split;   // index of the split within the sequence
+  int n_act;   // splits of the sequence (1: the workgroup writes the output itself)
+  int first;   // partial slot of split 0 of the sequence for this workgroup's KV head
+  int seqlen, qs, kv_end;
+  int k_lo, k_hi;
+};
+
+// Sequence of t tiles in n splits of equal size: the splits that hold keys.
+__device__ __forceinline__ int active_splits(int t, int n) {
+  if (t <= 0) return 1;
+  return ceil_div_small(t, ceil_div_small(t, n));
+}
+
+// Partition of every sequence's keys into splits of equal size (whole 32-key tiles).
+//   * Fixed (chunk > 0, grid (n_splits, Hkv, B)): sequence b gets
+//     n = ceil(tiles / chunk tiles) splits, capped at kMaxDecodeSplits.
+//   * Balanced (chunk == 0, B <= 64, grid (S, Hkv, 1)): sequence b gets
+//     n_b = min(kMaxDecodeSplits, ceil(t_b / C)) splits, with C the smallest tile
+//     count per split (>= 4) for which the splits of all sequences fit in the S
+//     slots; the slots are handed out in sequence order. The cost of one workgroup
+//     is then at most C tiles whatever the mix of lengths, where a per-sequence
+//     chunk gives the short sequences half-empty workgroups. Every workgroup
+//     evaluates the same integer search (binary, on one wave's lanes, one lane per
+//     sequence), so all of them agree on the partition.
+template <bool PAGED>
+__device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
+  DecodePart dp;
+  if (p.chunk > 0) {
+    dp.b = blockIdx.z;
+    dp.split = blockIdx.x;
+    const SeqInfo si = seq_info<PAGED>(p, dp.b, 0);
+    const int t = (si.kv_end + 31) >> 5;
+    const int ct = p.chunk >> 5;
+    const int n = max(1, min(kMaxDecodeSplits, (t + ct - 1) / ct));
+    const int size = (t + n - 1) / n;
+    dp.n_act = active_splits(t, n);
+    dp.first = (blockIdx.y * p.B + dp.b) * p.n_splits;  // n_splits slots per (KV head, sequence)
+    dp.seqlen = si.seqlen;
+    dp.qs = si.qs;
+    dp.kv_end = si.kv_end;
+    dp.k_lo = dp.split * size * 32;
+    dp.k_hi = min(si.kv_end, dp.k_lo + size * 32);
+    if (dp.split >= dp.n_act) dp.b = -1;
+    return dp;
+  }
+  const int lane = threadIdx.x & 63;
+  const bool has = lane < p.B;
+  SeqInfo sl;
+  sl.seqlen = sl.qs = sl.kv_end = 0;
+  if (has) sl = seq_info<PAGED>(p, lane, 0);
+  const int t = (sl.kv_end + 31) >> 5;
+  const int S = p.n_splits;
+  // splits of a sequence for C tiles per split (an empty sequence still takes one
+  // slot); the count over-estimates only where the cap of kMaxDecodeSplits bites
+  auto splits_of = [&](int C) { return max(1, min(kMaxDecodeSplits, ceil_div_small(t, C))); };
+  auto count = [&](int C) { return wave_sum_i32(has ? splits_of(C) : 0); };
+  const int T = wave_sum_i32(t);
+  // C = ceil(T / S) is a lower bound; ceil(T / (S - B)) fits, as each sequence
+  // rounds up by less than one split (the host sizes S so that C = 160 fits).
+  const int nb = min(p.B, 64);
+  int lo = min(kDecodeMaxTiles, max(4, ceil_div_small(T, S)));
+  int hi = S > nb ? min(kDecodeMaxTiles, max(lo, ceil_div_small(T, S - nb))) : kDecodeMaxTiles;
+  while (lo < hi) {
+    const int mid = (lo + hi) >> 1;
+    if (count(mid) <= S) hi = mid;
+    else lo = mid + 1;
+  }
+  const int n_split = splits_of(lo);
+  const int n_l = has ? active_splits(t, n_split) : 0;
+  const int size_l = t > 0 ? ceil_div_small(t, n_split) : 0;
+  const int incl = wave_incl_scan_i32(n_l);
+  const int slot = blockIdx.x;
+  const uint64_t mine = __builtin_amdgcn_ballot_w64(has && incl > slot);
+  if (mine == 0) {
+    dp.b = -1;
+    return dp;
+  }
+  const int b = static_cast<int>(__builtin_ctzll(mine));
+  dp.b = b;
+  dp.n_act = __builtin_amdgcn_readlane(n_l, b);
+  const int first = __builtin_amdgcn_readlane(incl, b) - dp.n_act;
+  dp.split = slot - first;
+  dp.first = blockIdx.y * S + first;  // S slots per KV head
+  dp.seqlen = __builtin_amdgcn_readlane(sl.seqlen, b);
+  dp.qs = __builtin_amdgcn_readlane(sl.qs, b);
+  dp.kv_end = __builtin_amdgcn_readlane(sl.kv_end, b);
+  const int size = __builtin_amdgcn_readlane(size_l, b);
+  dp.k_lo = dp.split * size * 32;
+  dp.k_hi = min(dp.kv_end, dp.k_lo + size * 32);
+  return dp;
+}
+
+// Merge of the split partials of one (sequence, KV head) unit, run by the last
+// workgroup of the unit to finish. One work item per (row, 16 columns), so the
+// 64-row worst case takes one pass of 512 threads; the splits are folded in
+// groups of eight whose loads are all issued before any is used (one memory
+// round trip up to eight splits), with the running maximum moved between groups.
+template <bool F16>
+__device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh, int64_t slot0, int n_act, int tid,
+                                             int nthreads) {
+  constexpr int D = 128;
+  constexpr int GS = 8;
+  const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot0 * 64 * D, 0, n_act * 64 * D * 4, kBufferFlags);
+  const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot0 * 64, 0, n_act * 64 * 8, kBufferFlags);
+  for (int item = tid; item < p.R * 8; item += nthreads) {
+    // columns 4 c8 + 32 j + (0..3), j = 0..3: the eight threads of a row read 128
+    // contiguous bytes per load
+    const int r = item >> 3;
+    const int c8 = (item & 7) * 4;
+    float m = -INFINITY, l = 0.f;
+    f32x4 o[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) o[j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < n_act; s0 += GS) {
+      float2 ml[GS];
+      f32x4 x[GS][4];
+#pragma unroll
+      for (int u = 0; u < GS; ++u) {
+        // splits past n_act read as zero (outside the descriptor) and weigh nothing
+        const int row = (s0 + u) * 64 + r;
+        ml[u] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(mrsrc, row * 8, 0, kSc1));
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          x[u][j] = __builtin_bit_cast(
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(orsrc, (row * D + c8 + 32 * j) * 4, 0, kSc1));
+      }
+      float mg = m;
+#pragma unroll
+      for (int u = 0; u < GS; ++u)
+        if (s0 + u < n_act) mg = fmaxf(mg, ml[u].x);
+      if (mg == -INFINITY) continue;  // nothing seen yet
+      const float a = m == -INFINITY ? 0.f : fast_exp2((m - mg) * p.scale_log2);
+      l *= a;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] *= a;
+#pragma unroll
+      for (int u = 0; u < GS; ++u) {
+        const float w = (s0 + u < n_act && ml[u].x != -INFINITY) ? fast_exp2((ml[u].x - mg) * p.scale_log2) : 0.f;
+        l += w * ml[u].y;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] += w * x[u][j];
+      }
+      m = mg;
+    }
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    const int t = r / p.G;
+    const int hh = r - t * p.G;
+    uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh + c8;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x2*>(orow + 32 * j) =
+          u32x2{pack2<F16>(o[j][0] * inv, o[j][1] * inv), pack2<F16>(o[j][2] * inv, o[j][3] * inv)};
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Split-KV decode attention, one (sequence, KV head, key range) per workgroup.
 //
@@ -757,7 +952,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
   constexpr int KS = D + 8;
   constexpr int VS = D + 16;
   constexpr int NDT = D / 16;
-  constexpr int kMaxPages = 160;
+  constexpr int kMaxPages = kDecodeMaxTiles;
   constexpr int KBUF = KT * KS;
   constexpr int VBUF = KT * VS;
   // [team][buffer] K then V tiles; reused for the team merge at the end
@@ -775,17 +970,20 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
   const int l16 = lane & 15;
   const int g = lane >> 4;
 
-  const int split = blockIdx.x;
   const int kvh = blockIdx.y;
-  const int b = blockIdx.z;
-  const SeqInfo si = seq_info<PAGED>(p, b, 0);
-  const int nsplit = max(1, (si.kv_end + p.chunk - 1) / p.chunk);
-  const int size = ((si.kv_end + nsplit - 1) / nsplit + KT - 1) / KT * KT;
-  const int n_act = size > 0 ? (si.kv_end + size - 1) / size : 0;
-  if (split >= max(n_act, 1)) return;
-  const int k_lo = split * size;
-  const int k_hi = min(si.kv_end, k_lo + size);
-  const int ntiles = k_hi > k_lo ? (k_hi - k_lo + KT - 1) / KT : 0;
+  const DecodePart dp = decode_partition<PAGED>(p);
+  if (dp.b < 0) return;  // idle slot (uniform over the workgroup)
+  const int b = __builtin_amdgcn_readfirstlane(dp.b);
+  const int split = __builtin_amdgcn_readfirstlane(dp.split);
+  const int n_act = __builtin_amdgcn_readfirstlane(dp.n_act);
+  const int k_lo = __builtin_amdgcn_readfirstlane(dp.k_lo);
+  const int k_hi = __builtin_amdgcn_readfirstlane(dp.k_hi);
+  SeqInfo si;
+  si.seqlen = dp.seqlen;
+  si.qs = dp.qs;
+  si.kv_end = dp.kv_end;
+  // at most kMaxPages tiles by construction of the partition (the min keeps LDS indexing in bounds)
+  const int ntiles = min(kMaxPages, k_hi > k_lo ? (k_hi - k_lo + KT - 1) / KT : 0);
   const int nsteps = (ntiles + 1) / 2;  // tiles per team, rounded up (both teams run every step)
 
   // ---- query fragments and row limits of this wave's 16 rows
@@ -966,8 +1164,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
     x[NDT * 4 + 1] = l_run;
   }
   lds_barrier();
-  if (team == 1) return;
-  {
+  if (team == 0) {
     const float* x = xfer + (wt * 64 + lane) * XS;
     const float m1 = x[NDT * 4];
     const float l1 = x[NDT * 4 + 1];
@@ -980,13 +1177,14 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
 #pragma unroll
       for (int j = 0; j < 4; ++j) acc[dt][j] = acc[dt][j] * a0 + x[dt * 4 + j] * a1;
     m_run = m_new;
+    l_run = group4_allreduce_sum(l_run);
   }
 
-  // ---- epilogue (team 0)
-  l_run = group4_allreduce_sum(l_run);
+  // ---- epilogue (team 0 holds the workgroup's result): rows r = 16 wt + l16,
+  // columns d = 16 dt + 4 g + j
   const int r = wt * 16 + l16;
   if (n_act <= 1) {
-    if (r < p.R) {
+    if (team == 0 && r < p.R) {
       const int t = r / p.G;
       const int hh = r - t * p.G;
       const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
@@ -999,73 +1197,34 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
     }
     return;
   }
-  if (r >= p.R) return;  // padding rows are never read
-  const int64_t slot = static_cast<int64_t>(b * p.Hkv + kvh) * p.n_splits + split;
-  float* po = p.ws_o + (slot * 64 + r) * D;
+  const int unit = b * p.Hkv + kvh;
+  const int64_t slot0 = dp.first;  // partial slot of split 0 of this unit
+  if (team == 0 && r < p.R) {  // padding rows are never read
+    const int64_t slot = slot0 + split;
+    const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot * 64 * D, 0, 64 * D * 4, kBufferFlags);
 #pragma unroll
-  for (int dt = 0; dt < NDT; ++dt) *reinterpret_cast<f32x4*>(po + dt * 16 + g * 4) = acc[dt];
-  if (g == 0) p.ws_ml[slot * 64 + r] = make_float2(m_run, l_run);
-}
-
-// Merge of kv_split_decode_kernel's partials: one thread per (row, 8 columns);
-// every split's (m, l) and partial row are loaded before any is used, so the
-// merge costs one memory round trip.
-template <bool F16, bool PAGED>
-__global__ __launch_bounds__(256) void kv_split_combine_kernel(const AttnParams p) {
-  constexpr int D = 128;
-  constexpr int MAXS = kMaxDecodeSplits;
-  const int unit = blockIdx.y;  // b * Hkv + kvh
-  const int b = unit / p.Hkv;
-  const int kvh = unit - b * p.Hkv;
-  const int r = blockIdx.x * 16 + (threadIdx.x >> 4);
-  if (r >= p.R) return;
-  const SeqInfo si = seq_info<PAGED>(p, b, 0);
-  const int nsplit = max(1, (si.kv_end + p.chunk - 1) / p.chunk);
-  const int size = ((si.kv_end + nsplit - 1) / nsplit + 31) / 32 * 32;
-  const int n_act = size > 0 ? (si.kv_end + size - 1) / size : 0;
-  if (n_act <= 1) return;  // written by the attention kernel
-  const int d0 = (threadIdx.x & 15) * 8;
-  const int64_t base = static_cast<int64_t>(unit) * p.n_splits * 64 + r;
-  float2 ml[MAXS];
-  f32x4 x0[MAXS], x1[MAXS];
-#pragma unroll
-  for (int s = 0; s < MAXS; ++s) {
-    if (s < n_act) {
-      const int64_t sl = base + static_cast<int64_t>(s) * 64;
-      ml[s] = p.ws_ml[sl];
-      const f32x4* po = reinterpret_cast<const f32x4*>(p.ws_o + sl * D + d0);
-      x0[s] = po[0];
-      x1[s] = po[1];
+    for (int dt = 0; dt < NDT; ++dt)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[dt]), orsrc, (r * D + dt * 16 + g * 4) * 4,
+                                             0, kSc1);
+    if (g == 0) {
+      const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot * 64, 0, 64 * 8, kBufferFlags);
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)), mrsrc, r * 8, 0,
+                                            kSc1);
     }
   }
-  float m = -INFINITY;
-#pragma unroll
-  for (int s = 0; s < MAXS; ++s)
-    if (s < n_act) m = fmaxf(m, ml[s].x);
-  float l = 0.f;
-  float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (m != -INFINITY) {
-#pragma unroll
-    for (int s = 0; s < MAXS; ++s) {
-      if (s < n_act) {
-        const float w = ml[s].x == -INFINITY ? 0.f : fast_exp2((ml[s].x - m) * p.scale_log2);
-        l += w * ml[s].y;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          o[j] += w * x0[s][j];
-          o[4 + j] += w * x1[s][j];
-        }
-      }
-    }
-  }
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  const int t = r / p.G;
-  const int hh = r - t * p.G;
-  uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh + d0;
-  u32x4 w4;
-#pragma unroll
-  for (int j = 0; j < 4; ++j) w4[j] = pack2<F16>(o[2 * j] * inv, o[2 * j + 1] * inv);
-  *reinterpret_cast<u32x4*>(orow) = w4;
+  // The last workgroup of the unit to arrive merges every split. The partials were
+  // written with device-coherent stores; waiting for their acknowledgement before the
+  // arrival is counted (one device-scope atomic) publishes them, and the merge reads
+  // them back with device-coherent loads.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  __shared__ int s_last;
+  if (tid == 0)
+    s_last = __hip_atomic_fetch_add(&p.ws_cnt[unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_act - 1;
+  __syncthreads();
+  if (!s_last) return;
+  merge_splits<F16>(p, b, kvh, slot0, n_act, tid, 512);
+  if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
 }
 
 // Merge the split partials of every (sequence, KV head, row block) with more than
@@ -1195,11 +1354,13 @@ struct Plan {
   size_t ws_o_bytes, ws_ml_bytes;
 };
 
-// Split-KV decode plan: keys per workgroup such that sequences of the longest
-// length would give about kSplitTargetWG workgroups (one per CU), within
-// [128, kMaxDecodeSplits splits of the longest sequence].
-constexpr int kSplitTargetWG = 256;
-constexpr int kSplitMaxChunk = 5120;  // 160 page ids of 32-key tiles in LDS
+// Split-KV decode plan. By default the kernel partitions the keys itself from the
+// device-side lengths (balanced mode) over S slots per KV head, S * Hkv ~ one
+// workgroup per CU; a caller-given kv_split fixes the keys per split instead.
+constexpr int kSplitTargetWG = 256;                   // MI355X compute units
+constexpr int kSplitMaxChunk = kDecodeMaxTiles * 32;  // keys per split: page ids staged in LDS
+constexpr int kBalancedMaxBatch = 64;                 // one wave lane per sequence in the partition search
+constexpr size_t kCounterBytes = 64 * 1024;           // arrival counters at the head of the workspace
 
 int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
   FDLLM_CHECK_ARG(d != nullptr, "fdllm_kv_attn: null descriptor");
@@ -1239,29 +1400,37 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
                             ? std::min<int64_t>(d->max_seqlen, static_cast<int64_t>(d->max_pages) * d->page_size)
                             : d->max_seqlen;
     const int64_t len = std::max(1, max_len);
-    int64_t chunk;
-    if (d->kv_split > 0) {
-      chunk = d->kv_split;
-    } else {
-      const int64_t total = static_cast<int64_t>(std::max(d->batch, 1)) * d->num_kv_heads * len;
-      chunk = (total + kSplitTargetWG - 1) / kSplitTargetWG;
-      chunk = std::max<int64_t>(chunk, 128);
-    }
-    chunk = std::max<int64_t>(chunk, (len + kMaxDecodeSplits - 1) / kMaxDecodeSplits);
-    chunk = (chunk + 31) / 32 * 32;
-    chunk = std::min<int64_t>(chunk, (len + 31) / 32 * 32);
-    if (chunk <= kSplitMaxChunk) {
+    const int64_t max_t = (len + 31) / 32;  // tiles of the longest sequence
+    // every split holds at most kDecodeMaxTiles tiles and a sequence at most kMaxDecodeSplits splits
+    if (max_t <= static_cast<int64_t>(kDecodeMaxTiles) * kMaxDecodeSplits &&
+        static_cast<int64_t>(d->batch) * hkv <= static_cast<int64_t>(kCounterBytes / sizeof(int))) {
+      const int64_t B = std::max(d->batch, 1);
+      const int64_t min_splits = (max_t + kDecodeMaxTiles - 1) / kDecodeMaxTiles;  // of the longest sequence
       pl->kind = kPlanSplitDecode;
       pl->decode = false;
       pl->MT = 1;
       pl->rows_per_wg = 64;
       pl->n_rb = 1;
-      pl->chunk = static_cast<int>(chunk);
-      pl->n_splits = static_cast<int>((len + chunk - 1) / chunk);
-      const int64_t units = static_cast<int64_t>(d->batch) * hkv;
-      if (pl->n_splits > 1) {
-        pl->ws_o_bytes = static_cast<size_t>(units) * pl->n_splits * 64 * d->head_dim * sizeof(float);
-        pl->ws_ml_bytes = static_cast<size_t>(units) * pl->n_splits * 64 * sizeof(float2);
+      int64_t slots;  // partial slots per KV head
+      bool split_possible;
+      if (d->kv_split == 0 && B <= kBalancedMaxBatch) {
+        pl->chunk = 0;
+        slots = std::max<int64_t>((kSplitTargetWG + hkv - 1) / hkv, B * min_splits);
+        pl->n_splits = static_cast<int>(slots);
+        split_possible = slots > B;
+      } else {
+        int64_t chunk = d->kv_split > 0 ? d->kv_split : kSplitMaxChunk;
+        chunk = std::max<int64_t>(chunk, (max_t + kMaxDecodeSplits - 1) / kMaxDecodeSplits * 32);
+        chunk = std::min<int64_t>(chunk, kSplitMaxChunk);
+        pl->chunk = static_cast<int>(chunk);
+        pl->n_splits = static_cast<int>((max_t * 32 + chunk - 1) / chunk);  // per sequence
+        slots = B * pl->n_splits;
+        split_possible = pl->n_splits > 1;
+      }
+      FDLLM_CHECK_ARG(slots * hkv < (int64_t{1} << 31) / 64, "fdllm_kv_attn: too many split slots");
+      if (split_possible) {
+        pl->ws_o_bytes = static_cast<size_t>(slots) * hkv * 64 * d->head_dim * sizeof(float);
+        pl->ws_ml_bytes = static_cast<size_t>(slots) * hkv * 64 * sizeof(float2);
       } else {
         pl->ws_o_bytes = pl->ws_ml_bytes = 0;
       }
@@ -1390,6 +1559,16 @@ void launch_attn(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
   }
 }
 
+// Workspace layout: a fixed 64 KiB of arrival counters (one int per (sequence,
+// KV head)), the (m, l) pairs of every split partial, then the partial rows. The
+// counter region has the same place and size for every call, so partials of one
+// call never land where a later call with more sequences keeps its counters.
+inline size_t counter_bytes(const fdllm_kv_attn_desc*) { return kCounterBytes; }
+
+inline size_t plan_workspace_bytes(const fdllm_kv_attn_desc* d, const Plan& pl) {
+  return pl.ws_o_bytes > 0 ? counter_bytes(d) + align256(pl.ws_ml_bytes) + pl.ws_o_bytes : 0;
+}
+
 }  // namespace
 }  // namespace fdllm
 
@@ -1399,7 +1578,7 @@ extern "C" int fdllm_kv_attn_workspace_size(const fdllm_kv_attn_desc* desc, size
   Plan pl;
   const int rc = make_plan(desc, &pl);
   if (rc != FDLLM_OK) return rc;
-  *bytes = pl.n_splits > 1 ? align256(pl.ws_ml_bytes) + pl.ws_o_bytes : 0;
+  *bytes = plan_workspace_bytes(desc, pl);
   return FDLLM_OK;
 }
 
@@ -1418,7 +1597,7 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
                       d->v_stride_page % 8 == 0 && d->v_stride_slot % 8 == 0 && d->v_stride_h % 8 == 0 &&
                       d->out_stride_b % 8 == 0 && d->out_stride_s % 8 == 0 && d->out_stride_h % 8 == 0,
                   "fdllm_kv_attn_fwd: strides must be multiples of 8 elements");
-  const size_t need = pl.n_splits > 1 ? align256(pl.ws_ml_bytes) + pl.ws_o_bytes : 0;
+  const size_t need = plan_workspace_bytes(d, pl);
   if (need > 0) {
     if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)) {
       set_last_error("fdllm_kv_attn_fwd: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
@@ -1468,9 +1647,12 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
   p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
   if (need > 0) {
     char* w = static_cast<char*>(workspace);
+    p.ws_cnt = reinterpret_cast<int*>(w);
+    w += counter_bytes(d);
     p.ws_ml = reinterpret_cast<float2*>(w);
     p.ws_o = reinterpret_cast<float*>(w + align256(pl.ws_ml_bytes));
   } else {
+    p.ws_cnt = nullptr;
     p.ws_ml = nullptr;
     p.ws_o = nullptr;
   }
@@ -1478,23 +1660,13 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (pl.kind == kPlanSplitDecode) {
     const bool paged = p.page_table != nullptr;
-    const dim3 grid(pl.n_splits, d->num_kv_heads, d->batch);
+    const dim3 grid(pl.n_splits, d->num_kv_heads, pl.chunk > 0 ? d->batch : 1);
     if (f16) {
       if (paged) kv_split_decode_kernel<kDecodeStages, true, true><<<grid, dim3(512), 0, s>>>(p);
       else kv_split_decode_kernel<kDecodeStages, true, false><<<grid, dim3(512), 0, s>>>(p);
     } else {
       if (paged) kv_split_decode_kernel<kDecodeStages, false, true><<<grid, dim3(512), 0, s>>>(p);
       else kv_split_decode_kernel<kDecodeStages, false, false><<<grid, dim3(512), 0, s>>>(p);
-    }
-    if (pl.n_splits > 1) {
-      const dim3 cgrid((pl.R + 15) / 16, static_cast<unsigned>(grid_z));
-      if (f16) {
-        if (paged) kv_split_combine_kernel<true, true><<<cgrid, dim3(256), 0, s>>>(p);
-        else kv_split_combine_kernel<true, false><<<cgrid, dim3(256), 0, s>>>(p);
-      } else {
-        if (paged) kv_split_combine_kernel<false, true><<<cgrid, dim3(256), 0, s>>>(p);
-        else kv_split_combine_kernel<false, false><<<cgrid, dim3(256), 0, s>>>(p);
-      }
     }
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }

@@ -50,9 +50,10 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 class _Workspace:
     """Scratch per (device, stream), grown on demand and reused.
 
-    The split-KV attention writes every partial it later merges, so the buffer
-    needs no clearing between calls; calls on one stream run in order and may
-    share it.
+    The buffer is zero-filled when allocated: the split-KV decode kernel's
+    arrival counters must start at zero, and every call leaves them at zero.
+    Partials are written before they are read, so nothing else needs clearing;
+    calls on one stream run in order and may share the buffer.
     """
 
     def __init__(self) -> None:

@@ -166,11 +166,15 @@ typedef struct fdllm_kv_attn_desc {
 #define FDLLM_ATTN_ALL_HEADS_DECODE 2
 
 /* Bytes of device workspace fdllm_kv_attn_fwd needs for `desc` (0 when the call
- * is not split over several workgroups per KV head). The workspace holds the
- * per-split partial results (running max, sum and unnormalised output rows) that
- * a second kernel merges; every call writes what it reads, so the contents need
- * no initialisation and one workspace serves any sequence of calls of any sizes.
- * Calls that may overlap in time (different streams) need separate workspaces. */
+ * is not split over several workgroups per KV head). The workspace starts with
+ * 64 KiB of arrival counters (one int per (sequence, KV head)), followed by the
+ * per-split partial results (running max, sum and unnormalised output rows); the
+ * last workgroup of a KV head to finish (or, for non-decode shapes, a second
+ * kernel) merges them. The workspace must be zero-filled once when it is
+ * allocated: every call leaves the counters at zero again and writes every
+ * partial it reads, so one workspace then serves any sequence of calls of any
+ * sizes. Calls that may overlap in time (different streams) need separate
+ * workspaces. */
 int fdllm_kv_attn_workspace_size(const fdllm_kv_attn_desc* desc, size_t* bytes);
 
 /* Launch the attention described by `desc` on `stream`. */

@@ -190,6 +190,84 @@ def test_repeated_split_calls_rearm(gpu):
     assert torch.equal(first, again)
 
 
+@pytest.mark.parametrize("case", ["batch80_fixed_chunks", "one_long_capped", "batch64_all_lanes", "hkv1_256_slots"])
+def test_split_decode_partitions(gpu, case):
+    """The split decode kernel's key partition at its edges: more than 64 sequences (fixed
+    5120-key chunks), one sequence long enough to need the 16-split cap next to empty and
+    one-tile sequences, exactly 64 sequences (every lane of the search), and one KV head
+    (256 slots per head)."""
+    g = torch.Generator().manual_seed(len(case))
+    hq, hkv = 28, 4
+    if case == "batch80_fixed_chunks":
+        lens = torch.randint(1, 400, (80,), generator=g)
+        lens[3], lens[50] = 5200, 5121
+    elif case == "one_long_capped":
+        lens = torch.tensor([0, 20000, 31, 32, 33])
+    elif case == "batch64_all_lanes":
+        lens = torch.randint(0, 700, (64,), generator=g)
+    else:
+        hq, hkv = 4, 1
+        lens = torch.randint(100, 3000, (20,), generator=g)
+    B, D, Sq = len(lens), 128, 8
+    max_s = int(lens.max())
+    q = torch.randn(B, Sq, hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, max_s, hkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, max_s, hkv, D, generator=g).to(torch.bfloat16)
+    sl = lens.to(torch.int32)
+    print(f"case partition {case} B={B} max_len={max_s}", flush=True)
+    if case == "batch80_fixed_chunks":
+        # a split call with few sequences first fills the workspace right after the
+        # counter region; the 320 counters of this call must not read those partials
+        small = workloads.kv_decode_paged(seed=9, batch=4, min_prefix=2048, max_prefix=4096)
+        ops.block_attn(small.q.to(gpu), small.k_pool.to(gpu), small.v_pool.to(gpu), small.seqlens.to(gpu),
+                       small.scale, page_table=small.page_table.to(gpu), page_size=small.page_size)
+    out = ops.block_attn(q.to(gpu), k.to(gpu), v.to(gpu), sl.to(gpu))
+    _check(out, oa.attention_np(q.float(), k.float(), v.float(), sl))
+
+
+def test_split_decode_counters_rearm_under_graph_replay(gpu):
+    """The split decode kernel's last workgroup per KV head merges the partials and
+    resets that head's arrival counter: after every call the counters read zero, and a
+    captured call replayed several times (eager calls of another size in between)
+    matches the eager result on every replay."""
+    wl = workloads.kv_decode_paged(seed=6, batch=16, min_prefix=2048, max_prefix=4096)
+    q, kp, vp = wl.q.to(gpu), wl.k_pool.to(gpu), wl.v_pool.to(gpu)
+    pt, sl = wl.page_table.to(gpu), wl.seqlens.to(gpu)
+    other = workloads.kv_decode_paged(seed=7, batch=3, min_prefix=700, max_prefix=3000)
+    oq, okp, ovp = other.q.to(gpu), other.k_pool.to(gpu), other.v_pool.to(gpu)
+    opt, osl = other.page_table.to(gpu), other.seqlens.to(gpu)
+
+    def call():
+        return ops.block_attn(q, kp, vp, sl, wl.scale, page_table=pt, page_size=wl.page_size)
+
+    def other_call():
+        return ops.block_attn(oq, okp, ovp, osl, other.scale, page_table=opt, page_size=other.page_size)
+
+    eager = call()
+    _check(eager, oa.attention_np(wl.q.float(), wl.k_pool.float(), wl.v_pool.float(), wl.seqlens, wl.scale,
+                                  page_table=wl.page_table, page_size=wl.page_size))
+    other_eager = other_call()
+    torch.cuda.synchronize(gpu)
+    units = q.shape[0] * kp.shape[2]
+    ws = ops._WORKSPACE.get(0, gpu)
+    assert int(ws[:4 * units].view(torch.int32).abs().sum()) == 0, "arrival counters not reset"
+    s = torch.cuda.Stream(gpu)
+    s.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(s):
+        call()  # workspace for this stream exists before capture
+        torch.cuda.synchronize(gpu)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            out = call()
+    torch.cuda.current_stream(gpu).wait_stream(s)
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        assert torch.equal(out, eager)
+        assert torch.equal(other_call(), other_eager)
+        torch.cuda.synchronize(gpu)
+
+
 def test_workspace_reuse_across_shapes(gpu):
     """One workspace serves consecutive split calls of different sizes: a large call
     after a small one must not merge partials the small call left behind."""
