@@ -924,14 +924,13 @@ __device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh
 // per KV head, which gives a grid of a few hundred workgroups whose partial
 // results are only the 64 rows of one KV head.
 //   * Workgroup = 8 waves in two teams of 4. Team tm takes the 32-key tiles
-//     t = 2j + tm of the range, so a workgroup keeps 8 waves busy (16 per CU at
-//     two workgroups per CU) without a second split of the keys; wave w of a team
-//     owns query rows 16w .. 16w + 15. The two teams' running results are merged
-//     through LDS at the end.
-//   * The key range of a sequence is cut into n = ceil(kv_end / chunk) equal
-//     splits (multiples of 32 keys), so the workgroups of one sequence do equal
-//     work; the grid is sized for the longest sequence and surplus workgroups
-//     exit at once.
+//     t = 2j + tm of the range, so a workgroup keeps 8 waves busy without a
+//     second split of the keys; wave w of a team owns query rows 16w .. 16w + 15.
+//     The two teams' running results are merged through LDS at the end.
+//   * The keys of each sequence are cut into equal splits of whole 32-key tiles
+//     (decode_partition): balanced over the grid's slots from the device-side
+//     lengths by default, or a fixed number of keys per split; slots without a
+//     split exit at once.
 //   * Staging: each thread owns 2 K and 2 V 16-byte chunks of its team's tile,
 //     fetched NS tiles ahead into registers with buffer loads whose descriptor
 //     covers only the keys below k_hi: rows past the end read as zero without
@@ -943,8 +942,11 @@ __device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh
 //   * Math as in kv_decode_kernel, one 16-row M-tile per wave: S^T = K Q^T with
 //     v_mfma_f32_16x16x32_bf16, online softmax with a lazily moved reference max,
 //     O^T += V^T P^T with the V^T operand from ds_read_b64_tr_b16.
-//   * A single-split unit writes its output rows; otherwise the unnormalised
-//     partial (O, m, l) goes to the workspace for kv_split_combine_kernel.
+//   * A single-split unit writes its output rows. Otherwise each workgroup
+//     writes its unnormalised partial (O, m, l) to the workspace with
+//     device-coherent stores, waits for them to complete and counts its arrival
+//     with one atomic; the last workgroup of the unit merges all partials
+//     (merge_splits) and resets the counter, so no second kernel is launched.
 template <int NS, bool F16, bool PAGED>
 __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParams p) {
   constexpr int D = 128;
