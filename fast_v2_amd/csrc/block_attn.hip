@@ -1229,6 +1229,252 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
   if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <bool F16>
+__device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
+  if constexpr (F16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Prefill attention: many query rows per KV head (block-causal prefill and
+// commit forwards), head_dim 128, no key split.
+//
+// Workgroup = 8 waves = 256 query rows of one (sequence, KV head), rows
+// r = t * G + hh in token order, 32 rows per wave (two waves per SIMD); keys in
+// 64-key tiles, each read once per workgroup and used by all 256 rows.
+//   * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: A = 32 keys x 16 d read from LDS,
+//     B = Q^T held in registers for the whole loop (lane (n, h) = row n, d
+//     16 ks + 8 h .. + 8). Accumulator lane (n, h), element 4 i + j = row n,
+//     key 8 i + 4 h + j of the 32-key subtile.
+//   * O^T += V^T P^T on the same instruction. Its k-slot e of lane half h stands
+//     for key 4 h + e (e < 4) or 8 + 4 h + (e - 4) of a 16-key step, so the P^T
+//     operand is eight consecutive accumulator elements as they are, and the V^T
+//     operand is two ds_read_b64_tr_b16 of four keys each.
+//   * Online softmax in base 2: the row max is shared by the two lane halves of a
+//     row; the reference max moves only when it would be exceeded by more than
+//     8 / log2-scale, so exponentials stay below 2^8 and most tiles skip the
+//     rescale of the 64 accumulators.
+//   * Staging: every thread owns 2 K and 2 V 16-byte chunks of a tile, fetched two
+//     tiles ahead into registers by buffer loads whose descriptor ends at the
+//     last visible key (rows past it read as zero without traffic), then stored
+//     to one of two padded LDS buffers; one barrier per tile.
+//   * Grid (B * Hkv, row blocks), row blocks in reverse so the longest key ranges
+//     start first; workgroup ids of one (sequence, KV head) differ by a multiple
+//     of B * Hkv, which keeps its row blocks on one XCD (and its K/V in one L2)
+//     when B * Hkv is a multiple of 8.
+template <bool F16, bool PAGED>
+__global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) {
+  constexpr int D = 128;
+  constexpr int KT = 64;
+  constexpr int KS = D + 8;   // K row stride in LDS: 16-byte pad
+  constexpr int VS = D + 16;  // V row stride in LDS: 32-byte pad for the transposing reads
+  constexpr int KBUF = KT * KS;
+  constexpr int VBUF = KT * VS;
+  __shared__ __attribute__((aligned(16))) uint16_t sKV[2][KBUF + VBUF];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int n32 = lane & 31;
+  const int h = lane >> 5;
+  const int l16 = lane & 15;
+  const int g16 = lane >> 4;
+
+  const int unit = blockIdx.x;
+  const int b = unit / p.Hkv;
+  const int kvh = unit - b * p.Hkv;
+  const int rb = p.n_rb - 1 - static_cast<int>(blockIdx.y);
+  const SeqInfo si = seq_info<PAGED>(p, b, rb);
+  const int row0 = rb * 256;
+  const int kv_end = si.kv_end;
+  const int ntiles = (kv_end + KT - 1) / KT;
+
+  // ---- this lane's query row: Q^T fragments and key limit
+  const int r = row0 + wave * 32 + n32;
+  const int rc = min(r, p.R - 1);  // padding rows reuse a valid row: finite, never written
+  const int t = rc / p.G;
+  const int hh = rc - t * p.G;
+  const int lim = row_key_limit(p, si.seqlen, si.qs, t);
+  u32x4 qf[8];
+  {
+    const uint16_t* qrow = p.q + b * p.q_sb + t * p.q_ss + (kvh * p.G + hh) * p.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * h);
+  }
+  const int lim_min =
+      __builtin_amdgcn_readfirstlane(-static_cast<int>(wave_allreduce_max(-static_cast<float>(lim))));
+  const int lim_max = __builtin_amdgcn_readfirstlane(static_cast<int>(wave_allreduce_max(static_cast<float>(lim))));
+  const float c2 = p.scale_log2;
+  const float rescale_thr = 8.f / c2;
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // ---- staging: chunk c = tid + 512 i of a tile is key c / 16, 16-byte column c % 16
+  const int krow_bytes = static_cast<int>(p.k_ss) * 2;
+  const int vrow_bytes = static_cast<int>(p.v_ss) * 2;
+  int koff[2], voff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 512 * i;
+    koff[i] = (c >> 4) * krow_bytes + (c & 15) * 16;
+    voff[i] = (c >> 4) * vrow_bytes + (c & 15) * 16;
+  }
+  const uint16_t* kbase = p.k + kvh * p.k_sh + (PAGED ? 0 : b * p.k_sp);
+  const uint16_t* vbase = p.v + kvh * p.v_sh + (PAGED ? 0 : b * p.v_sp);
+  const int32_t* pt_row = PAGED ? p.page_table + static_cast<int64_t>(b) * p.max_pages : nullptr;
+  struct Stage {
+    u32x4 k[2];
+    u32x4 v[2];
+  };
+  Stage st0, st1;
+
+  auto load_tile = [&](Stage& sg, int j) {
+    const int kb = j * KT;
+    const int valid = __builtin_amdgcn_readfirstlane(max(0, min(KT, kv_end - kb)));
+    int64_t koffs, voffs;
+    if constexpr (PAGED) {
+      // page_size >= 64 and tiles start at multiples of 64: one page per tile
+      const int page = pt_row[min(kb >> p.page_shift, p.max_pages - 1)];
+      const int slot0 = kb & (p.page_size - 1);
+      koffs = static_cast<int64_t>(page) * p.k_sp + slot0 * p.k_ss;
+      voffs = static_cast<int64_t>(page) * p.v_sp + slot0 * p.v_ss;
+    } else {
+      koffs = static_cast<int64_t>(kb) * p.k_ss;
+      voffs = static_cast<int64_t>(kb) * p.v_ss;
+    }
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase + koffs), 0, valid * krow_bytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase + voffs), 0, valid * vrow_bytes, kBufferFlags);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      sg.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0));
+      sg.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, 0));
+    }
+  };
+  auto store_tile = [&](const Stage& sg, int buf) {
+    uint16_t* sk = sKV[buf];
+    uint16_t* sv = sk + KBUF;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 512 * i;
+      *reinterpret_cast<u32x4*>(&sk[(c >> 4) * KS + (c & 15) * 8]) = sg.k[i];
+      *reinterpret_cast<u32x4*>(&sv[(c >> 4) * VS + (c & 15) * 8]) = sg.v[i];
+    }
+  };
+  auto compute_tile = [&](int buf, int kb) {
+    const uint16_t* sk = sKV[buf];
+    const uint16_t* sv = sk + KBUF;
+    f32x16 s[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[st][e] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(&sk[(32 * st + n32) * KS + 16 * ks + 8 * h]);
+        s[st] = mfma32x32x16<F16>(kf, qf[ks], s[st]);
+      }
+    }
+    if (!(kb + KT <= lim_min)) {  // wave-uniform: some row of the wave sees part of the tile
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (kb + 32 * st + 8 * i + 4 * h + j >= lim) s[st][4 * i + j] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[st][e]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + rescale_thr) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = m_run == -INFINITY ? 0.f : fast_exp2((m_run - m_new) * c2);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = m_run == -INFINITY ? 0.f : m_run * c2;
+    float lsum = 0.f;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float v = fast_exp2(fmaf(s[st][e], c2, -mc));
+        s[st][e] = v;
+        lsum += v;
+      }
+    l_run += lsum;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int st = kk >> 1;
+      const int e0 = 8 * (kk & 1);
+      const u32x4 pf = {pack2<F16>(s[st][e0], s[st][e0 + 1]), pack2<F16>(s[st][e0 + 2], s[st][e0 + 3]),
+                        pack2<F16>(s[st][e0 + 4], s[st][e0 + 5]), pack2<F16>(s[st][e0 + 6], s[st][e0 + 7])};
+      const int vr = 16 * kk + 4 * (g16 >> 1) + (l16 >> 2);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const int vc = 32 * dt + 16 * (g16 & 1) + 4 * (l16 & 3);
+        const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(&sv[vr * VS + vc]));
+        const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(&sv[(vr + 8) * VS + vc]));
+        acc[dt] = mfma32x32x16<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf, acc[dt]);
+      }
+    }
+  };
+
+  // Every step stores, synchronises and issues its loads whether or not its tile
+  // exists (loads past the range are zero-filled without traffic), so the loads in
+  // flight are the same on every path; only the math is conditional.
+  auto step = [&](Stage& sg, int j) {
+    store_tile(sg, j & 1);
+    lds_barrier();
+    load_tile(sg, j + 2);
+    const int kb = j * KT;
+    if (j < ntiles && kb < lim_max) compute_tile(j & 1, kb);  // wave-uniform
+  };
+  if (ntiles > 0) {
+    load_tile(st0, 0);
+    load_tile(st1, 1);
+    for (int j = 0; j < ntiles; j += 2) {
+      step(st0, j);
+      step(st1, j + 1);
+    }
+  }
+
+  // ---- epilogue: rows of both lane halves are whole after the exchange of l
+  l_run += __shfl_xor(l_run, 32, kWave);
+  if (r < p.R) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 4 * i;
+        *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i + 4 * h) =
+            u32x2{pack2<F16>(acc[dt][e] * inv, acc[dt][e + 1] * inv),
+                  pack2<F16>(acc[dt][e + 2] * inv, acc[dt][e + 3] * inv)};
+      }
+  }
+}
+
 // Merge the split partials of every (sequence, KV head, row block) with more than
 // one active split. 8 output columns per thread, D / 8 threads per row.
 template <int D, bool F16, bool PAGED>
@@ -1347,7 +1593,7 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 
 // Workspace layout: the (m, l) pairs of every split partial, then the partial
 // rows. Nothing needs to be zero: each call writes every slot it later reads.
-enum PlanKind { kPlanGeneral = 0, kPlanAllHeads = 1, kPlanSplitDecode = 2 };
+enum PlanKind { kPlanGeneral = 0, kPlanAllHeads = 1, kPlanSplitDecode = 2, kPlanPrefill = 3 };
 
 struct Plan {
   int kind;     // PlanKind
@@ -1468,6 +1714,21 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
     } else {
       pl->ws_o_bytes = pl->ws_ml_bytes = 0;
     }
+    return FDLLM_OK;
+  }
+  // Prefill shapes: at least 8 row blocks of 256 per KV head, pages of >= 64 keys
+  const bool prefill_shape = !(d->flags & FDLLM_ATTN_NO_DECODE_KERNEL) && d->head_dim == 128 &&
+                             pl->R >= 8 * 256 && d->kv_split == 0 &&
+                             (d->page_table == nullptr || d->page_size >= 64) && d->k_stride_slot < (1 << 24) &&
+                             d->v_stride_slot < (1 << 24) && (pl->R + 255) / 256 < 65536;
+  if (prefill_shape) {
+    pl->kind = kPlanPrefill;
+    pl->MT = 4;
+    pl->rows_per_wg = 256;
+    pl->n_rb = (pl->R + 255) / 256;
+    pl->n_splits = 1;
+    pl->chunk = 1 << 30;
+    pl->ws_o_bytes = pl->ws_ml_bytes = 0;
     return FDLLM_OK;
   }
   const int mtiles = (pl->R + 15) / 16;
@@ -1669,6 +1930,18 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
     } else {
       if (paged) kv_split_decode_kernel<kDecodeStages, false, true><<<grid, dim3(512), 0, s>>>(p);
       else kv_split_decode_kernel<kDecodeStages, false, false><<<grid, dim3(512), 0, s>>>(p);
+    }
+    FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
+  }
+  if (pl.kind == kPlanPrefill) {
+    const bool paged = p.page_table != nullptr;
+    const dim3 grid(static_cast<unsigned>(grid_z), pl.n_rb);
+    if (f16) {
+      if (paged) kv_prefill_kernel<true, true><<<grid, dim3(512), 0, s>>>(p);
+      else kv_prefill_kernel<true, false><<<grid, dim3(512), 0, s>>>(p);
+    } else {
+      if (paged) kv_prefill_kernel<false, true><<<grid, dim3(512), 0, s>>>(p);
+      else kv_prefill_kernel<false, false><<<grid, dim3(512), 0, s>>>(p);
     }
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }

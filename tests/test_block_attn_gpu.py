@@ -339,3 +339,62 @@ def test_decode_kernel_vs_general(gpu, hq, hkv, q_len, paged):
             outs.append(o.float().cpu())
     for o in outs[1:]:
         torch.testing.assert_close(o, outs[0], atol=2e-2, rtol=2e-2)
+
+
+def _paginate(k, v, page_size, g):
+    """Contiguous [B, S, Hkv, D] caches -> a shuffled page pool and its page table."""
+    B, S, Hkv, D = k.shape
+    per = (S + page_size - 1) // page_size
+    perm = torch.randperm(B * per, generator=g)
+    kp = torch.zeros(B * per, page_size, Hkv, D, dtype=k.dtype)
+    vp = torch.zeros_like(kp)
+    pt = torch.zeros(B, per, dtype=torch.int32)
+    for b in range(B):
+        for i in range(per):
+            pg = int(perm[b * per + i])
+            pt[b, i] = pg
+            n = min(page_size, S - i * page_size)
+            kp[pg, :n] = k[b, i * page_size:i * page_size + n]
+            vp[pg, :n] = v[b, i * page_size:i * page_size + n]
+    return kp, vp, pt
+
+
+@pytest.mark.parametrize("case", [
+    "gqa7_block_causal_prefix",   # 28/4 heads, cached prefix + new rows, block-causal
+    "gqa7_fp16_paged64",          # the same in fp16 over 64-key pages
+    "mha_causal_paged256",        # 8/8 heads (G = 1), causal, 256-key pages
+    "gqa8_full_ragged",           # 16/2 heads, every key visible, ragged lengths
+    "gqa4_block64_one_head",      # 4/1 heads, 64-key blocks
+])
+def test_prefill_kernel(gpu, case):
+    """The prefill kernel (>= 2048 query rows per KV head) against the float64 oracle
+    across head groupings, masks, dtypes, paging, cached prefixes and row counts that
+    are not multiples of its 256-row blocks."""
+    g = torch.Generator().manual_seed(sum(map(ord, case)))
+    dtype, page, mode, blk = torch.bfloat16, 0, _ffi.MASK_BLOCK_CAUSAL, 32
+    if case == "gqa7_block_causal_prefix":
+        B, Sq, hq, hkv, lens = 2, 300, 28, 4, [812, 300]
+    elif case == "gqa7_fp16_paged64":
+        B, Sq, hq, hkv, lens, dtype, page = 2, 300, 28, 4, [812, 333], torch.float16, 64
+    elif case == "mha_causal_paged256":
+        B, Sq, hq, hkv, lens, mode, page = 1, 2100, 8, 8, [2400], _ffi.MASK_CAUSAL, 256
+    elif case == "gqa8_full_ragged":
+        B, Sq, hq, hkv, lens, mode = 2, 600, 16, 2, [900, 650], _ffi.MASK_SEQLEN
+    else:
+        B, Sq, hq, hkv, lens, blk = 1, 1000, 4, 1, [1000], 64
+    D, max_s = 128, max(lens)
+    q = torch.randn(B, Sq, hq, D, generator=g).to(dtype)
+    k = torch.randn(B, max_s, hkv, D, generator=g).to(dtype)
+    v = torch.randn(B, max_s, hkv, D, generator=g).to(dtype)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    print(f"case prefill {case}", flush=True)
+    if page:
+        kc, vc, pt = _paginate(k, v, page, g)
+        args = dict(page_table=pt.to(gpu), page_size=page)
+    else:
+        kc, vc, args = k, v, {}
+    exp = oa.attention_np(q.float(), k.float(), v.float(), sl, mask_mode=mode, mask_block=blk)
+    for prefill in (True, False):  # False: the general kernel on the same call
+        out = ops.block_attn(q.to(gpu), kc.to(gpu), vc.to(gpu), sl.to(gpu), mask_mode=mode, mask_block=blk,
+                             decode_kernel=prefill, **args)
+        _check(out, exp)
