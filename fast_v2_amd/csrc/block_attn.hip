@@ -1231,6 +1231,18 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
+// max / sum of the values of lanes l and l ^ 32 (v_permlane32_swap_b32: both
+// results hold lanes 0-31 of one operand and lanes 32-63 of the other, so each
+// lane ends up with its own value and its partner's)
+__device__ __forceinline__ float halves_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 template <bool F16>
 __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
   if constexpr (F16) {
@@ -1402,7 +1414,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
     for (int st = 0; st < 2; ++st)
 #pragma unroll
       for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[st][e]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+    mx = halves_max(mx);
     if (__builtin_amdgcn_ballot_w64(mx > m_run + rescale_thr) != 0) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = m_run == -INFINITY ? 0.f : fast_exp2((m_run - m_new) * c2);
@@ -1459,7 +1471,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
   }
 
   // ---- epilogue: rows of both lane halves are whole after the exchange of l
-  l_run += __shfl_xor(l_run, 32, kWave);
+  l_run = halves_sum(l_run);
   if (r < p.R) {
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
     uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh;

@@ -51,8 +51,11 @@ struct Elt<bf16_t> {
   static constexpr int kBytes = 2;
   __device__ __forceinline__ static float lo(uint32_t w) { return __uint_as_float(w << 16); }
   __device__ __forceinline__ static float hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+  // one v_cvt_pk_bf16_f32 (RNE), the same rounding as two single conversions
   __device__ __forceinline__ static uint32_t pack(float a, float b) {
-    return f32_to_bf16_bits(a) | (f32_to_bf16_bits(b) << 16);
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, bf16x2));
   }
   __device__ __forceinline__ static float round(float a) {
     return bf16_bits_to_f32(f32_to_bf16_bits(a));
@@ -64,7 +67,9 @@ struct Elt<f16_t> {
   __device__ __forceinline__ static float lo(uint32_t w) { return f16_bits_to_f32(w & 0xffffu); }
   __device__ __forceinline__ static float hi(uint32_t w) { return f16_bits_to_f32(w >> 16); }
   __device__ __forceinline__ static uint32_t pack(float a, float b) {
-    return f32_to_f16_bits(a) | (f32_to_f16_bits(b) << 16);
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
   }
   __device__ __forceinline__ static float round(float a) {
     return f16_bits_to_f32(f32_to_f16_bits(a));
