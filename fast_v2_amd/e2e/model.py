@@ -42,19 +42,52 @@ class BlockDiffusionConfig:
         return self.hidden_size // self.num_attention_heads
 
 
+_IDENTITY_ROWS: dict = {}
+
+
+def _identity_rows(n: int, device) -> torch.Tensor:
+    """int64 [1, n] = 0 .. n-1, cached per (n, device) (the gather index of a plain norm)."""
+    key = (n, str(device))
+    t = _IDENTITY_ROWS.get(key)
+    if t is None:
+        t = torch.arange(n, dtype=torch.int64, device=device)[None]
+        _IDENTITY_ROWS[key] = t
+    return t
+
+
 class RMSNorm(nn.Module):
-    """w * (x.f32 * rsqrt(mean(x.f32^2) + eps)).to(dtype) (modeling.py:427-432)."""
+    """w * (x.f32 * rsqrt(mean(x.f32^2) + eps)).to(dtype) (modeling.py:427-432).
+
+    With ``fused`` set (the HIP implementation sets it while the model is patched),
+    the norm runs as one gather + RMSNorm kernel over all rows in the same rounding
+    order (the model-path mode of fused_sparse_extension.py:51-87), instead of the
+    eight elementwise and reduction kernels of the torch statement."""
 
     def __init__(self, hidden_size: int, eps: float):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(hidden_size))
         self.variance_epsilon = eps
+        self.fused = False
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.fused:
+            from .. import _ffi, ops
+            shape = x.shape
+            rows = x.reshape(1, -1, shape[-1])
+            normed, _ = ops.gather_rmsnorm(rows, _identity_rows(rows.shape[1], x.device), self.weight,
+                                           self.variance_epsilon, _ffi.NORM_WEIGHT_AFTER_CAST, with_gathered=False)
+            return normed.view(shape)
         dt = x.dtype
         h = x.float()
         h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + self.variance_epsilon)
         return self.weight * h.to(dt)
+
+
+def set_fused_norms(model: nn.Module, on: bool) -> None:
+    """Switch every RMSNorm of ``model`` to the fused kernel (or back to torch)."""
+    for mod in model.modules():
+        if isinstance(mod, RMSNorm):
+            mod.fused = on
 
 
 class Attention(nn.Module):
@@ -193,4 +226,4 @@ def param_count(cfg: BlockDiffusionConfig) -> int:
     return v * h * 2 + L * per_layer + h
 
 
-__all__ = ["BlockDiffusionConfig", "BlockDiffusionLM", "build_model", "param_count", "RMSNorm"]
+__all__ = ["BlockDiffusionConfig", "BlockDiffusionLM", "build_model", "param_count", "RMSNorm", "set_fused_norms"]

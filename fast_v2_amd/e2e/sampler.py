@@ -31,12 +31,19 @@ import torch
 
 from ..utils.attention_backends import get_attention_backend, patch_attention_layers, unpatch_attention_layers
 from ..utils.static_kv_cache import StaticBlockCache, StaticKVCache
+from .model import set_fused_norms
 
 
 class HipStaticAttention:
-    """StaticKVCache / StaticBlockCache with HIP writes + the 'hip' attention backend."""
+    """StaticKVCache / StaticBlockCache with HIP writes + the 'hip' attention backend,
+    the model's RMSNorms on the fused gather + RMSNorm kernel, and the diffusion-step
+    forwards replayed from HIP graphs (``graphs=False`` runs them eagerly)."""
 
     name = "hip"
+
+    def __init__(self, graphs: bool = True, fused_norm: bool = True):
+        self.graphs = graphs
+        self.fused_norm = fused_norm
 
     def make_caches(self, batch, max_seq_len, cfg, dtype, device, use_block_cache):
         cache = StaticKVCache(batch, max_seq_len, cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim,
@@ -46,10 +53,53 @@ class HipStaticAttention:
         return cache, block
 
     def patch(self, model, block_cache):
+        if self.fused_norm:
+            set_fused_norms(model, True)
         return patch_attention_layers(model, get_attention_backend("hip"), block_cache)
 
     def unpatch(self, model, originals):
         unpatch_attention_layers(model, originals)
+        set_fused_norms(model, False)
+
+
+class ForwardGraphs:
+    """One HIP graph per kind of diffusion-step forward (the full block, and the
+    sub-block at each offset), captured on first use and replayed after that.
+
+    Everything that changes between blocks reaches the captured kernels through
+    device memory: the token ids and positions are copied into the graph's static
+    inputs before each replay, and the static cache's write position and visible
+    lengths live in device tensors (StaticKVCache.kv_write_start / scratch_seqlens).
+    Commits advance host-side state and run eagerly. The first use of a kind runs
+    it eagerly once (on the capture stream, so allocations and the attention
+    workspace exist before capture), captures it, and replays it; the eager run and
+    the replay write the same cache rows."""
+
+    def __init__(self):
+        self._graphs = {}
+        self._stream = None
+
+    def __call__(self, key, fn, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        ent = self._graphs.get(key)
+        if ent is None:
+            if self._stream is None:
+                self._stream = torch.cuda.Stream(ids.device)
+            s = self._stream
+            sid, spos = ids.clone(), pos.clone()
+            s.wait_stream(torch.cuda.current_stream(ids.device))
+            with torch.cuda.stream(s):
+                fn(sid, spos)
+            torch.cuda.current_stream(ids.device).wait_stream(s)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=s):
+                out = fn(sid, spos)
+            ent = (graph, sid, spos, out)
+            self._graphs[key] = ent
+        graph, sid, spos, out = ent
+        sid.copy_(ids)
+        spos.copy_(pos)
+        graph.replay()
+        return out
 
 
 @dataclass
@@ -106,6 +156,7 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
         return tok
 
     impl = impl or HipStaticAttention()
+    graphs = ForwardGraphs() if getattr(impl, "graphs", False) else None
     cfg = model.config
     B, P = input_ids.shape
     dev = input_ids.device
@@ -151,14 +202,25 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
                     if not bool(mask[:, s0:s1].any()):
                         break
                     if use_block_cache and len(block_cache) > 0 and not bool(mask[:, s0].any()):
-                        logits = model(x[:, blk][:, s0:s1], cache, use_block_cache=True,
-                                       block_past_key_values=block_cache, replace_position=s0,
-                                       logits_to_keep=small_block_size)
+                        def sub_fwd(ids, pos, s0=s0):
+                            return model(ids, cache, use_block_cache=True, block_past_key_values=block_cache,
+                                         replace_position=s0, cache_position=pos, logits_to_keep=small_block_size)
+                        ids = x[:, blk][:, s0:s1]
+                        pos = cache_pos[s0:s1]
+                        logits = graphs(("sub", s0), sub_fwd, ids, pos) if graphs else sub_fwd(ids, pos)
                         logits = torch.cat([logits[:, :1], logits[:, :-1]], dim=1)
                     else:
-                        logits = model(x[:, blk], cache, use_block_cache=use_block_cache,
-                                       block_past_key_values=block_cache, cache_position=cache_pos,
-                                       logits_to_keep=block_size)
+                        def full_fwd(ids, pos):
+                            return model(ids, cache, use_block_cache=use_block_cache,
+                                         block_past_key_values=block_cache, cache_position=pos,
+                                         logits_to_keep=block_size)
+                        if graphs:
+                            logits = graphs(("full",), full_fwd, x[:, blk], cache_pos)
+                            if block_cache is not None:
+                                # the replay wrote every layer's block rows (StaticBlockCache.update)
+                                block_cache._num_initialized = cfg.num_hidden_layers
+                        else:
+                            logits = full_fwd(x[:, blk], cache_pos)
                         logits = torch.cat([logits[:, :1], logits[:, :-1]], dim=1)[:, s0:s1]
                     stats.forwards += 1
                     tok, conf = greedy_with_confidence(logits)
@@ -193,4 +255,5 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
         impl.unpatch(model, originals)
 
 
-__all__ = ["generate", "greedy_with_confidence", "threshold_unmask", "HipStaticAttention", "GenerationStats"]
+__all__ = ["generate", "greedy_with_confidence", "threshold_unmask", "HipStaticAttention", "ForwardGraphs",
+           "GenerationStats"]

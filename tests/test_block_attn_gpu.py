@@ -362,6 +362,7 @@ def _paginate(k, v, page_size, g):
 @pytest.mark.parametrize("case", [
     "gqa7_block_causal_prefix",   # 28/4 heads, cached prefix + new rows, block-causal
     "gqa7_fp16_paged64",          # the same in fp16 over 64-key pages
+    "gqa7_paged32",               # 32-key pages: the general kernel takes the call
     "mha_causal_paged256",        # 8/8 heads (G = 1), causal, 256-key pages
     "gqa8_full_ragged",           # 16/2 heads, every key visible, ragged lengths
     "gqa4_block64_one_head",      # 4/1 heads, 64-key blocks
@@ -376,6 +377,8 @@ def test_prefill_kernel(gpu, case):
         B, Sq, hq, hkv, lens = 2, 300, 28, 4, [812, 300]
     elif case == "gqa7_fp16_paged64":
         B, Sq, hq, hkv, lens, dtype, page = 2, 300, 28, 4, [812, 333], torch.float16, 64
+    elif case == "gqa7_paged32":
+        B, Sq, hq, hkv, lens, page = 2, 300, 28, 4, [700, 333], 32
     elif case == "mha_causal_paged256":
         B, Sq, hq, hkv, lens, mode, page = 1, 2100, 8, 8, [2400], _ffi.MASK_CAUSAL, 256
     elif case == "gqa8_full_ragged":

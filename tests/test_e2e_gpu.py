@@ -127,6 +127,31 @@ def _forced_rate(model, x, N, use_block_cache, rec, hip, impl):
 
 
 @pytest.mark.parametrize("use_block_cache", [True, False])
+def test_graph_replay_matches_eager_forwards(gpu, use_block_cache):
+    """The HIP-graph replays of the diffusion forwards give the same generation as the
+    same forwards run eagerly (same kernels, same inputs), token for token, and the
+    fused RMSNorm matches the torch statement of the norm to bf16 rounding."""
+    cfg = _small_cfg()
+    model = em.build_model(cfg, gpu)
+    x = _prompts(4, 64, cfg.vocab_size, seed=2).to(gpu)
+    eager, _ = es.generate(model, x, max_new_tokens=96, use_block_cache=use_block_cache,
+                           impl=es.HipStaticAttention(graphs=False))
+    graphed, st = es.generate(model, x, max_new_tokens=96, use_block_cache=use_block_cache,
+                              impl=es.HipStaticAttention(graphs=True))
+    print(f"block cache {use_block_cache}: {st.forwards} forwards")
+    assert torch.equal(eager, graphed)
+    h = torch.randn(4, 32, cfg.hidden_size, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(gpu)
+    norm = model.model.layers[0].input_layernorm
+    ref = norm(h)
+    norm.fused = True
+    try:
+        got = norm(h)
+    finally:
+        norm.fused = False
+    torch.testing.assert_close(got.float(), ref.float(), atol=1e-2, rtol=1e-2)
+
+
+@pytest.mark.parametrize("use_block_cache", [True, False])
 def test_generation_agreement_small(gpu, use_block_cache):
     """2-layer model, batch 4, 64-token prompts, 96 new tokens."""
     cfg = _small_cfg()
