@@ -67,6 +67,26 @@ ATTN_NO_DECODE_KERNEL = 1
 ATTN_ALL_HEADS_DECODE = 2
 
 
+class RopeKVDesc(ctypes.Structure):
+    """Mirror of ``fdllm_rope_kv_desc`` (include/fdllm_hip.h)."""
+
+    _fields_ = [
+        ("q", _c_vp), ("q_stride_b", _c_i64), ("q_stride_s", _c_i64), ("q_stride_h", _c_i64),
+        ("k", _c_vp), ("k_stride_b", _c_i64), ("k_stride_s", _c_i64), ("k_stride_h", _c_i64),
+        ("v", _c_vp), ("v_stride_b", _c_i64), ("v_stride_s", _c_i64), ("v_stride_h", _c_i64),
+        ("cos", _c_vp), ("sin", _c_vp), ("cs_stride_b", _c_i64), ("cs_stride_s", _c_i64),
+        ("q_out", _c_vp), ("qo_stride_b", _c_i64), ("qo_stride_s", _c_i64), ("qo_stride_h", _c_i64),
+        ("k_out", _c_vp), ("v_out", _c_vp), ("ko_stride_b", _c_i64), ("ko_stride_s", _c_i64),
+        ("ko_stride_h", _c_i64),
+        ("k_cache", _c_vp), ("v_cache", _c_vp), ("c_stride_b", _c_i64), ("c_stride_s", _c_i64),
+        ("c_stride_h", _c_i64), ("cache_len", _c_i32), ("write_start", _c_vp), ("write_offset", _c_i32),
+        ("k_block", _c_vp), ("v_block", _c_vp), ("bc_stride_b", _c_i64), ("bc_stride_s", _c_i64),
+        ("bc_stride_h", _c_i64), ("block_len", _c_i32), ("block_offset", _c_i32),
+        ("batch", _c_i32), ("seq_len", _c_i32), ("num_q_heads", _c_i32), ("num_kv_heads", _c_i32),
+        ("head_dim", _c_i32), ("dtype", _c_i32),
+    ]
+
+
 # name -> (restype, argtypes); every symbol of include/fdllm_hip.h
 SIGNATURES = {
     "fdllm_abi_version": (_c_int, []),
@@ -96,6 +116,7 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int,         # B, T, Hkv, D
         _c_int, _c_vp,                          # dtype, stream
     ]),
+    "fdllm_rope_kv_write": (_c_int, [ctypes.POINTER(RopeKVDesc), _c_vp]),
 }
 
 _lib = None

@@ -275,6 +275,102 @@ def block_attn(
     return out
 
 
+def rope_kv_write(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    k_cache: Optional[torch.Tensor] = None,
+    v_cache: Optional[torch.Tensor] = None,
+    write_start: Optional[torch.Tensor] = None,
+    write_offset: int = 0,
+    k_block: Optional[torch.Tensor] = None,
+    v_block: Optional[torch.Tensor] = None,
+    block_offset: int = 0,
+    q_out: Optional[torch.Tensor] = None,
+    kv_out: bool = False,
+):
+    """RoPE of q and k fused with the cache writes (one kernel).
+
+    q [B, S, Hq, D], k / v [B, S, Hkv, D] (last dim contiguous), cos / sin [B or 1, S, D]
+    (or [S, D]) in the same 16-bit dtype. Returns ``q_rot`` (and ``(k_rot, v)`` copies
+    when ``kv_out``). The rotated k rows and the v rows go to ``k_cache``/``v_cache``
+    [B, L, Hkv, D] at ``write_start[b] + write_offset + t`` (``write_offset + t`` without
+    ``write_start``) and to ``k_block``/``v_block`` [B, Lb, Hkv, D] at ``block_offset + t``;
+    rows past a buffer's length are skipped. Rounding as the eager expression
+    ``q * cos + rotate_half(q) * sin`` (utils/attention_backends.py:777-788).
+    """
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4 or k.shape != v.shape:
+        raise RuntimeError("rope_kv_write: q [B,S,Hq,D], k / v [B,S,Hkv,D] expected")
+    B, S, Hq, D = q.shape
+    if k.shape[0] != B or k.shape[1] != S or k.shape[3] != D:
+        raise RuntimeError("rope_kv_write: q and k/v disagree in batch, length or head_dim")
+    Hkv = k.shape[2]
+    if cos.dim() == 2:
+        cos, sin = cos[None], sin[None]
+    if cos.shape != sin.shape or cos.dim() != 3 or cos.shape[1] != S or cos.shape[2] != D or \
+            cos.shape[0] not in (1, B):
+        raise RuntimeError("rope_kv_write: cos / sin must be [1 or B, S, D]")
+    if (k_cache is None) != (v_cache is None) or (k_block is None) != (v_block is None):
+        raise RuntimeError("rope_kv_write: give k and v destinations together")
+    tensors = [q, k, v, cos, sin] + [t for t in (k_cache, v_cache, k_block, v_block, write_start, q_out)
+                                     if t is not None]
+    dev = _require_gpu(*tensors)
+    if q.dtype not in (torch.bfloat16, torch.float16) or any(
+            t.dtype != q.dtype for t in (k, v, cos, sin, k_cache, v_cache, k_block, v_block, q_out) if t is not None):
+        raise RuntimeError("rope_kv_write: all tensors must share one 16-bit dtype")
+    def last_contig(t):
+        return t if t.stride(-1) == 1 and all(st % 8 == 0 for st in t.stride()[:-1]) else t.contiguous()
+    q, k, v, cos, sin = (last_contig(t) for t in (q, k, v, cos, sin))
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache), ("k_block", k_block), ("v_block", v_block)):
+        if c is not None and (c.dim() != 4 or c.shape[0] != B or c.shape[2] != Hkv or c.shape[3] != D or
+                              c.stride(-1) != 1):
+            raise RuntimeError(f"rope_kv_write: {name} must be [B, L, Hkv, D] with a contiguous last dim")
+    if k_cache is not None and k_cache.stride() != v_cache.stride():
+        raise RuntimeError("rope_kv_write: k_cache and v_cache strides differ")
+    if k_block is not None and k_block.stride() != v_block.stride():
+        raise RuntimeError("rope_kv_write: k_block and v_block strides differ")
+    if write_start is not None and (write_start.dtype != torch.int32 or not write_start.is_contiguous()):
+        write_start = write_start.to(torch.int32).contiguous()
+    if q_out is None:
+        q_out = torch.empty((B, S, Hq, D), dtype=q.dtype, device=dev)
+    kv_o = (torch.empty((B, S, Hkv, D), dtype=q.dtype, device=dev),
+            torch.empty((B, S, Hkv, D), dtype=q.dtype, device=dev)) if kv_out else (None, None)
+    d = _ffi.RopeKVDesc()
+    d.q, (d.q_stride_b, d.q_stride_s, d.q_stride_h) = q.data_ptr(), q.stride()[:3]
+    d.k, (d.k_stride_b, d.k_stride_s, d.k_stride_h) = k.data_ptr(), k.stride()[:3]
+    d.v, (d.v_stride_b, d.v_stride_s, d.v_stride_h) = v.data_ptr(), v.stride()[:3]
+    d.cos, d.sin = cos.data_ptr(), sin.data_ptr()
+    d.cs_stride_b = cos.stride(0) if cos.shape[0] == B and B > 1 else 0
+    d.cs_stride_s = cos.stride(1)
+    if sin.stride()[:2] != cos.stride()[:2]:
+        sin = sin.contiguous()
+        cos = cos.contiguous()
+        d.cos, d.sin, d.cs_stride_s = cos.data_ptr(), sin.data_ptr(), cos.stride(1)
+        d.cs_stride_b = cos.stride(0) if cos.shape[0] == B and B > 1 else 0
+    d.q_out, (d.qo_stride_b, d.qo_stride_s, d.qo_stride_h) = q_out.data_ptr(), q_out.stride()[:3]
+    if kv_out:
+        d.k_out, d.v_out = kv_o[0].data_ptr(), kv_o[1].data_ptr()
+        d.ko_stride_b, d.ko_stride_s, d.ko_stride_h = kv_o[0].stride()[:3]
+    if k_cache is not None:
+        d.k_cache, d.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+        d.c_stride_b, d.c_stride_s, d.c_stride_h = k_cache.stride()[:3]
+        d.cache_len = k_cache.shape[1]
+        d.write_start = _ptr(write_start)
+        d.write_offset = int(write_offset)
+    if k_block is not None:
+        d.k_block, d.v_block = k_block.data_ptr(), v_block.data_ptr()
+        d.bc_stride_b, d.bc_stride_s, d.bc_stride_h = k_block.stride()[:3]
+        d.block_len = k_block.shape[1]
+        d.block_offset = int(block_offset)
+    d.batch, d.seq_len, d.num_q_heads, d.num_kv_heads, d.head_dim = B, S, Hq, Hkv, D
+    d.dtype = _ffi.dtype_code(q.dtype)
+    rc = _ffi.lib().fdllm_rope_kv_write(ctypes.byref(d), _ffi.stream_ptr(dev))
+    _ffi.check(rc, "fdllm_rope_kv_write")
+    return (q_out, kv_o) if kv_out else q_out
+
+
 def kv_cache_write(
     k_new: torch.Tensor,
     v_new: torch.Tensor,

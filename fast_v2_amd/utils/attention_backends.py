@@ -166,6 +166,55 @@ def _apply_rotary_pos_emb(q, k, cos, sin):
     return q * cos + q_rot * sin, k * cos + k_rot * sin
 
 
+# The patched forward uses ops.rope_kv_write where it applies (False: RoPE in torch
+# and separate cache writes, the statement of the reference's code).
+FUSED_ROPE_CACHE_WRITE = True
+
+
+def _fused_rope_cache_write(q, k, v, cos, sin, layer_idx, cache, update, block_cache, replace_position):
+    """RoPE + the cache writes of the patched forward in one kernel (ops.rope_kv_write);
+    returns the rotated q, or None (nothing done) where the call is not one of the
+    three forms below, which then take the unfused path.
+
+    * commit (update_past_key_values, no block cache): rows at the committed length;
+    * diffusion step, no block cache: rows at kv_write_start (write_scratch_compiled);
+    * diffusion step with the block cache: rows at block offset rp and at
+      kv_write_start + rp. The unfused path copies all block rows to the static cache
+      at kv_write_start after each write; every earlier write of this block already put
+      the other rows there, so writing the new rows alone leaves the same cache. The
+      first forward of a block (the block cache's update) must cover the whole block.
+    Writes through ops.kv_cache_write and the attention are unchanged."""
+    if not isinstance(cache, StaticKVCache) or q.dtype not in (torch.bfloat16, torch.float16) or \
+            q.shape[-1] % 16 != 0 or cos.dim() != 3:
+        return None
+    S = k.shape[1]
+    if update:
+        if block_cache is not None:
+            return None
+        start = cache.get_seq_length()
+        q_rot = ops.rope_kv_write(q, k, v, cos, sin, cache.key_cache[layer_idx], cache.value_cache[layer_idx],
+                                  write_offset=start)
+        cache.note_update(S, layer_idx)
+        cache.set_scratch_seqlens(start + S)
+        return q_rot
+    if block_cache is None:
+        return ops.rope_kv_write(q, k, v, cos, sin, cache.key_cache[layer_idx], cache.value_cache[layer_idx],
+                                 write_start=cache._write_start)
+    kb, vb = block_cache[layer_idx]
+    if len(block_cache) <= layer_idx:
+        if S != kb.shape[1]:
+            return None
+        rp = 0
+    else:
+        rp = 0 if replace_position is None else int(replace_position)
+    q_rot = ops.rope_kv_write(q, k, v, cos, sin, cache.key_cache[layer_idx], cache.value_cache[layer_idx],
+                              write_start=cache._write_start, write_offset=rp, k_block=kb, v_block=vb,
+                              block_offset=rp)
+    if len(block_cache) <= layer_idx:
+        block_cache.note_update(layer_idx)
+    return q_rot
+
+
 def _create_patched_attention_forward(attn_module, attn_backend, static_block_cache=None):
     """Attention forward over the static cache (attention_backends.py:791-898):
     q/k/v projections -> RoPE -> sub-block cache -> KV write -> block attention
@@ -190,6 +239,16 @@ def _create_patched_attention_forward(attn_module, attn_backend, static_block_ca
         k = attn_module.k_proj(hidden_states).view(hidden_shape)
         v = attn_module.v_proj(hidden_states).view(hidden_shape)
         cos, sin = position_embeddings
+
+        if attn_backend.name == AttentionBackend.HIP and FUSED_ROPE_CACHE_WRITE:
+            q = _fused_rope_cache_write(q, k, v, cos, sin, layer_idx, past_key_value, update_past_key_values,
+                                        block_past_key_values, replace_position)
+            if q is not None:
+                full_k, full_v = past_key_value.get_full_kv(layer_idx)
+                out = attn_backend.flash_kvcache_attention(q, full_k, full_v,
+                                                           cache_seqlens=past_key_value.scratch_seqlens,
+                                                           is_causal=False, scaling=scaling)
+                return attn_module.o_proj(out.reshape(*input_shape, -1))
         q, k = _apply_rotary_pos_emb(q, k, cos, sin)
 
         if block_past_key_values is not None:

@@ -101,6 +101,15 @@ class StaticKVCache:
             raise RuntimeError(f"StaticKVCache.update: {start} + {seq_len} exceeds max_seq_len {self.max_seq_len}")
         ops.kv_cache_write(key_states, value_states, self.key_cache[layer_idx], self.value_cache[layer_idx],
                            write_offset=start)
+        return self.note_update(seq_len, layer_idx)
+
+    def note_update(self, seq_len: int, layer_idx: int):
+        """The bookkeeping of ``update`` for rows a fused kernel already wrote at the
+        committed position: advance after the last layer; returns the views ``update``
+        returns."""
+        start = self._seq_len
+        if start + seq_len > self.max_seq_len:
+            raise RuntimeError(f"StaticKVCache.update: {start} + {seq_len} exceeds max_seq_len {self.max_seq_len}")
         if layer_idx == self.num_layers - 1:
             self._seq_len += seq_len
             self.cache_seqlens.fill_(self._seq_len)
@@ -244,6 +253,10 @@ class StaticBlockCache:
         if key_states.shape[1] > self.block_size:
             raise RuntimeError("StaticBlockCache.update: more tokens than the block holds")
         self.write(key_states, value_states, layer_idx, 0)
+        return self.note_update(layer_idx)
+
+    def note_update(self, layer_idx: int):
+        """The bookkeeping of ``update`` for rows a fused kernel already wrote."""
         if layer_idx >= self._num_initialized:
             self._num_initialized = layer_idx + 1
         return self.key_cache[layer_idx], self.value_cache[layer_idx]

@@ -207,6 +207,63 @@ int fdllm_kv_cache_write(const void* k_new, const void* v_new,
                          int batch, int num_tokens, int num_kv_heads, int head_dim,
                          int dtype, void* stream);
 
+/* -------------------------------------------------------------------------
+ * RoPE of the new queries and keys fused with the KV cache write (the step
+ * between the q/k/v projections and the attention).
+ *
+ *   for b < batch, t < seq_len:
+ *     q_out[b, t, h]  = rope(q[b, t, h])                 h < num_q_heads
+ *     kr              = rope(k[b, t, g])                 g < num_kv_heads
+ *     k_cache[b, write_start[b] + write_offset + t, g] = kr   (write_start may
+ *     v_cache[b, write_start[b] + write_offset + t, g] = v[b, t, g]      be NULL)
+ *     k_block[b, block_offset + t, g] = kr;  v_block likewise    (if k_block)
+ *     k_out[b, t, g] = kr;  v_out[b, t, g] = v[b, t, g]           (if k_out)
+ *
+ *   rope(x)[i] = x[i] * cos[i] + rotate_half(x)[i] * sin[i],
+ *   rotate_half(x) = (-x[D/2 .. D), x[0 .. D/2)),
+ * rounded to `dtype` after each product and after the sum: the arithmetic of the
+ * eager 16-bit expression q * cos + rotate_half(q) * sin, so the result equals it
+ * bit for bit. cos / sin are [cs_batch (1 or batch), seq_len, head_dim] in `dtype`
+ * (the model's position embeddings). The caches are contiguous-row
+ * [batch, len, heads, head_dim] buffers with the given strides; rows at or
+ * beyond cache_len / block_len are skipped. q_out may alias q.
+ *
+ * Replaces: apply_rotary_pos_emb + the static / block cache writes of the
+ * patched attention forward (utils/attention_backends.py:777-788, :843-878;
+ * static_kv_cache.py:218-229 write_scratch_compiled, :451-457 StaticBlockCache.update).
+ * ------------------------------------------------------------------------- */
+typedef struct fdllm_rope_kv_desc {
+  const void* q; /* [batch, seq_len, num_q_heads, head_dim] */
+  int64_t q_stride_b, q_stride_s, q_stride_h;
+  const void* k; /* [batch, seq_len, num_kv_heads, head_dim] */
+  int64_t k_stride_b, k_stride_s, k_stride_h;
+  const void* v;
+  int64_t v_stride_b, v_stride_s, v_stride_h;
+  const void* cos; /* [cs_batch, seq_len, head_dim] */
+  const void* sin;
+  int64_t cs_stride_b, cs_stride_s; /* cs_stride_b = 0 broadcasts one table */
+  void* q_out;
+  int64_t qo_stride_b, qo_stride_s, qo_stride_h;
+  void* k_out; /* optional [batch, seq_len, num_kv_heads, head_dim], with v_out */
+  void* v_out;
+  int64_t ko_stride_b, ko_stride_s, ko_stride_h;
+  void* k_cache; /* optional destination 1 (the static cache of this layer) */
+  void* v_cache;
+  int64_t c_stride_b, c_stride_s, c_stride_h;
+  int32_t cache_len;
+  const int32_t* write_start; /* [batch] or NULL */
+  int32_t write_offset;
+  void* k_block; /* optional destination 2 (the within-block cache of this layer) */
+  void* v_block;
+  int64_t bc_stride_b, bc_stride_s, bc_stride_h;
+  int32_t block_len;
+  int32_t block_offset;
+  int batch, seq_len, num_q_heads, num_kv_heads, head_dim;
+  int dtype; /* FDLLM_DTYPE_BF16 or FDLLM_DTYPE_F16 */
+} fdllm_rope_kv_desc;
+
+int fdllm_rope_kv_write(const fdllm_rope_kv_desc* desc, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif

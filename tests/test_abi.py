@@ -36,7 +36,7 @@ def lib():
 def test_header_declares_the_entry_points():
     names = _declared_functions()
     assert {"fdllm_gather_rmsnorm", "fdllm_scatter_rows", "fdllm_kv_attn_fwd",
-            "fdllm_kv_attn_workspace_size", "fdllm_kv_cache_write", "fdllm_abi_version",
+            "fdllm_kv_attn_workspace_size", "fdllm_kv_cache_write", "fdllm_rope_kv_write", "fdllm_abi_version",
             "fdllm_last_error"} <= names
 
 
@@ -73,6 +73,28 @@ def test_descriptor_layout_matches_c_struct():
     assert ctypes.sizeof(d) % 8 == 0
 
 
+@pytest.mark.parametrize("struct", ["fdllm_kv_attn_desc", "fdllm_rope_kv_desc"])
+def test_descriptor_offsets_match_the_c_compiler(tmp_path, struct):
+    """Every field offset and the size of the ctypes mirrors equal what gcc lays out
+    for the structs of include/fdllm_hip.h."""
+    from fast_v2_amd import _ffi
+    mirror = {"fdllm_kv_attn_desc": _ffi.KVAttnDesc, "fdllm_rope_kv_desc": _ffi.RopeKVDesc}[struct]
+    fields = [f[0] for f in mirror._fields_]
+    prog = tmp_path / "layout.c"
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{ROOT / "include" / "fdllm_hip.h"}"',
+             'int main(void) {', f'  printf("size %zu\\n", sizeof({struct}));']
+    lines += [f'  printf("{n} %zu\\n", offsetof({struct}, {n}));' for n in fields]
+    lines += ['  return 0;', '}']
+    prog.write_text("\n".join(lines) + "\n")
+    exe = tmp_path / "layout"
+    subprocess.run(["gcc", "-std=c99", "-o", str(exe), str(prog)], check=True)
+    got = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True, text=True,
+                                                        check=True).stdout.splitlines())
+    assert int(got["size"]) == ctypes.sizeof(mirror)
+    for n in fields:
+        assert int(got[n]) == getattr(mirror, n).offset, n
+
+
 def test_rejected_arguments_launch_nothing(lib):
     """Calls that fail validation return a negative code and set the error text."""
     from fast_v2_amd import _ffi
@@ -98,6 +120,16 @@ def test_rejected_arguments_launch_nothing(lib):
     rc = lib.fdllm_kv_cache_write(None, None, 0, 0, 0, None, None, 0, 0, 0, None, 0, 0, 0, None, 0, None,
                                   1, 1, 4, 128, _ffi.DTYPE_F32, None)
     assert rc == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    r = _ffi.RopeKVDesc()
+    r.batch, r.seq_len, r.num_q_heads, r.num_kv_heads, r.head_dim = 1, 1, 28, 4, 128
+    r.dtype = _ffi.DTYPE_F32
+    assert lib.fdllm_rope_kv_write(ctypes.byref(r), None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    assert b"dtype" in lib.fdllm_last_error()
+    r.dtype, r.head_dim = _ffi.DTYPE_BF16, 72  # not a multiple of 16
+    assert lib.fdllm_rope_kv_write(ctypes.byref(r), None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    r.head_dim = 128  # no tensors given
+    assert lib.fdllm_rope_kv_write(ctypes.byref(r), None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    assert b"null" in lib.fdllm_last_error()
 
 
 def test_workspace_size_for_the_decode_workload(lib):
