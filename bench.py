@@ -29,6 +29,7 @@ import json
 import os
 import statistics
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -271,13 +272,24 @@ def bench_e2e(torch, args):
     build_s = time.perf_counter() - t0
     g = torch.Generator().manual_seed(0)
     x = torch.randint(0, cfg.vocab_size - 1, (16, 512), generator=g).to(dev)
-    es.generate(model, x, max_new_tokens=64, use_block_cache=True)  # warm-up
+    # GEMM solutions: torch TunableOp benchmarks the hipBLASLt / rocBLAS candidates of
+    # every GEMM shape the warm-up meets (prefill, full block, sub-block, commit) and
+    # keeps the fastest; tuning is off again before the timed run
+    tun = torch.cuda.tunable
+    tun.enable(True)
+    tun.tuning_enable(True)
+    tun.set_filename(os.path.join(tempfile.gettempdir(), f"fdllm_tunableop_{os.getpid()}_%d.csv"))
+    es.generate(model, x, max_new_tokens=64, use_block_cache=True)  # warm-up (and GEMM tuning)
+    tun.tuning_enable(False)
     out, st = es.generate(model, x, max_new_tokens=args.e2e_tokens, use_block_cache=True)
+    tun.enable(False)
     res = {"tokens_per_s": round(st.tokens_per_second, 1), "generated_tokens": st.generated_tokens,
            "seconds": round(st.seconds, 3), "forwards": st.forwards, "commits": st.commits,
            "ms_per_forward": round(st.seconds * 1e3 / max(st.forwards, 1), 3),
            "tokens_per_step": round(sum(st.step_tokens) / max(len(st.step_tokens), 1), 3),
            "params": em.param_count(cfg), "model_build_s": round(build_s, 2),
+           "gemm_tuning": "torch TunableOp over hipBLASLt / rocBLAS solutions, tuned in the warm-up",
+           "forwards_graphed": "diffusion steps replayed from HIP graphs; commits eager",
            "config": "28 layers, hidden 3584, 28/4 heads, vocab 152064, bf16 random init; batch 16, prompt 512, "
                      f"{args.e2e_tokens} new tokens, block 32, sub-block 8, threshold 0.9 (p > 0.9), block cache on"}
     del model, out, x
