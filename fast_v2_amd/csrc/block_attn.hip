@@ -960,6 +960,10 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
   // [team][buffer] K then V tiles; reused for the team merge at the end
   __shared__ __attribute__((aligned(16))) uint16_t sKV[2][2][KBUF + VBUF];
   __shared__ int sPage[kMaxPages];
+  // the whole page table when it is small: read together with the lengths, so the
+  // page ids of the workgroup's range need no second round trip after the partition
+  constexpr int kPrefetchPages = 4096;
+  __shared__ int sAllPages[kPrefetchPages];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -973,6 +977,16 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
   const int g = lane >> 4;
 
   const int kvh = blockIdx.y;
+  const int n_pt = PAGED ? p.B * p.max_pages : 0;
+  const bool pt_prefetch = PAGED && n_pt <= kPrefetchPages;  // uniform
+  int pf[kPrefetchPages / 512];
+  if (pt_prefetch) {
+#pragma unroll
+    for (int u = 0; u < kPrefetchPages / 512; ++u) {
+      const int idx = tid + 512 * u;
+      pf[u] = idx < n_pt ? p.page_table[idx] : 0;
+    }
+  }
   const DecodePart dp = decode_partition<PAGED>(p);
   if (dp.b < 0) return;  // idle slot (uniform over the workgroup)
   const int b = __builtin_amdgcn_readfirstlane(dp.b);
@@ -1006,8 +1020,16 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
   const float rescale_thr = 8.f / p.scale_log2;
 
   if constexpr (PAGED) {
-    const int32_t* pt_row = p.page_table + static_cast<int64_t>(b) * p.max_pages;
-    for (int i = tid; i < ntiles; i += 512) sPage[i] = pt_row[(k_lo + i * KT) >> p.page_shift];
+    if (pt_prefetch) {
+#pragma unroll
+      for (int u = 0; u < kPrefetchPages / 512; ++u) {
+        const int idx = tid + 512 * u;
+        if (idx < n_pt) sAllPages[idx] = pf[u];
+      }
+    } else {
+      const int32_t* pt_row = p.page_table + static_cast<int64_t>(b) * p.max_pages;
+      for (int i = tid; i < ntiles; i += 512) sPage[i] = pt_row[(k_lo + i * KT) >> p.page_shift];
+    }
   }
 
   f32x4 acc[NDT];
@@ -1044,7 +1066,10 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
     const int valid = __builtin_amdgcn_readfirstlane(max(0, min(KT, k_hi - kb)));
     int64_t koffs, voffs;
     if constexpr (PAGED) {
-      const int page = __builtin_amdgcn_readfirstlane(sPage[min(t, max(ntiles - 1, 0))]);
+      const int tc = min(t, max(ntiles - 1, 0));
+      const int page = __builtin_amdgcn_readfirstlane(
+          pt_prefetch ? sAllPages[b * p.max_pages + min((k_lo + tc * KT) >> p.page_shift, p.max_pages - 1)]
+                      : sPage[tc]);
       const int slot0 = kb & (p.page_size - 1);
       koffs = static_cast<int64_t>(page) * p.k_sp + slot0 * p.k_ss;
       voffs = static_cast<int64_t>(page) * p.v_sp + slot0 * p.v_ss;
@@ -1603,8 +1628,7 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const KVWriteArgs a) {
 // ---------------------------------------------------------------------------
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
-// Workspace layout: the (m, l) pairs of every split partial, then the partial
-// rows. Nothing needs to be zero: each call writes every slot it later reads.
+// Kernel families a call can take (make_plan picks one per descriptor).
 enum PlanKind { kPlanGeneral = 0, kPlanAllHeads = 1, kPlanSplitDecode = 2, kPlanPrefill = 3 };
 
 struct Plan {

@@ -225,6 +225,19 @@ def test_split_decode_partitions(gpu, case):
     _check(out, oa.attention_np(q.float(), k.float(), v.float(), sl))
 
 
+@pytest.mark.parametrize("batch,page_size", [(16, 32), (40, 16)])
+def test_split_decode_page_table_staging(gpu, batch, page_size):
+    """Paged split decode with a page table small enough to be read whole at the start
+    (16 x 130 ids) and one too large for that (40 x 250 ids), which stages only the
+    workgroup's own page ids."""
+    wl = workloads.kv_decode_paged(seed=11, batch=batch, min_prefix=1024, max_prefix=3968, page_size=page_size)
+    print(f"case page table {tuple(wl.page_table.shape)}", flush=True)
+    out = ops.block_attn(wl.q.to(gpu), wl.k_pool.to(gpu), wl.v_pool.to(gpu), wl.seqlens.to(gpu), wl.scale,
+                         page_table=wl.page_table.to(gpu), page_size=page_size)
+    _check(out, oa.attention_np(wl.q.float(), wl.k_pool.float(), wl.v_pool.float(), wl.seqlens, wl.scale,
+                                page_table=wl.page_table, page_size=page_size))
+
+
 def test_split_decode_counters_rearm_under_graph_replay(gpu):
     """The split decode kernel's last workgroup per KV head merges the partials and
     resets that head's arrival counter: after every call the counters read zero, and a
