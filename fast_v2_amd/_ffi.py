@@ -117,6 +117,14 @@ SIGNATURES = {
         _c_int, _c_vp,                          # dtype, stream
     ]),
     "fdllm_rope_kv_write": (_c_int, [ctypes.POINTER(RopeKVDesc), _c_vp]),
+    "fdllm_unmask_step": (_c_int, [
+        _c_vp, _c_i64, _c_i64, _c_int,          # logits, batch stride, row stride, vocab
+        _c_int, _c_int,                         # row_offset, shift
+        _c_vp, _c_i64,                          # tokens (int64), batch stride
+        _c_vp, _c_i64, _c_float, _c_i64,        # finished (uint8), mask_id, threshold, stop_token
+        _c_vp, _c_vp, _c_vp,                    # row_tok, row_conf, counts
+        _c_int, _c_int, _c_int, _c_vp,          # batch, positions, dtype, stream
+    ]),
 }
 
 _lib = None

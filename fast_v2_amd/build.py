@@ -21,7 +21,7 @@ LIB_DIR = PKG_DIR / "lib"
 LIB_PATH = LIB_DIR / "libfdllm_hip.so"
 HEADER = REPO_DIR / "include" / "fdllm_hip.h"
 
-SOURCES = [CSRC / "gather_rmsnorm.hip", CSRC / "block_attn.hip", CSRC / "rope_kv.hip"]
+SOURCES = [CSRC / "gather_rmsnorm.hip", CSRC / "block_attn.hip", CSRC / "rope_kv.hip", CSRC / "sampler.hip"]
 DEPS = SOURCES + [CSRC / "fdllm_common.h", HEADER]
 
 ARCH = "gfx950"

@@ -29,6 +29,7 @@ from typing import Optional
 
 import torch
 
+from .. import ops
 from ..utils.attention_backends import get_attention_backend, patch_attention_layers, unpatch_attention_layers
 from ..utils.static_kv_cache import StaticBlockCache, StaticKVCache
 from .model import set_fused_norms
@@ -41,9 +42,10 @@ class HipStaticAttention:
 
     name = "hip"
 
-    def __init__(self, graphs: bool = True, fused_norm: bool = True):
+    def __init__(self, graphs: bool = True, fused_norm: bool = True, fused_sampler: bool = True):
         self.graphs = graphs
         self.fused_norm = fused_norm
+        self.fused_sampler = fused_sampler
 
     def make_caches(self, batch, max_seq_len, cfg, dtype, device, use_block_cache):
         cache = StaticKVCache(batch, max_seq_len, cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim,
@@ -157,6 +159,8 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
 
     impl = impl or HipStaticAttention()
     graphs = ForwardGraphs() if getattr(impl, "graphs", False) else None
+    fused = getattr(impl, "fused_sampler", False) and policy is None
+    scratch = None
     cfg = model.config
     B, P = input_ids.shape
     dev = input_ids.device
@@ -197,32 +201,48 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
             blk = slice(block_idx * block_size, (block_idx + 1) * block_size)
             for sb in range(block_size // small_block_size):
                 s0, s1 = sb * small_block_size, (sb + 1) * small_block_size
-                while True:
-                    mask = x[:, blk] == mask_id
-                    if not bool(mask[:, s0:s1].any()):
-                        break
-                    if use_block_cache and len(block_cache) > 0 and not bool(mask[:, s0].any()):
+                # sub-block state: masked positions left (unfinished rows) and whether
+                # position s0 is still masked in some row; the fused sampler reports both
+                # after each step, the torch rule recomputes them from x
+                mask = x[:, blk] == mask_id
+                left = bool((mask[:, s0:s1] & ~finished[:, None]).any())
+                first_masked = bool(mask[:, s0].any())
+                while left:
+                    if use_block_cache and len(block_cache) > 0 and not first_masked:
                         def sub_fwd(ids, pos, s0=s0):
                             return model(ids, cache, use_block_cache=True, block_past_key_values=block_cache,
                                          replace_position=s0, cache_position=pos, logits_to_keep=small_block_size)
                         ids = x[:, blk][:, s0:s1]
                         pos = cache_pos[s0:s1]
-                        logits = graphs(("sub", s0), sub_fwd, ids, pos) if graphs else sub_fwd(ids, pos)
-                        logits = torch.cat([logits[:, :1], logits[:, :-1]], dim=1)
+                        raw = graphs(("sub", s0), sub_fwd, ids, pos) if graphs else sub_fwd(ids, pos)
+                        row_offset = 0
                     else:
                         def full_fwd(ids, pos):
                             return model(ids, cache, use_block_cache=use_block_cache,
                                          block_past_key_values=block_cache, cache_position=pos,
                                          logits_to_keep=block_size)
                         if graphs:
-                            logits = graphs(("full",), full_fwd, x[:, blk], cache_pos)
+                            raw = graphs(("full",), full_fwd, x[:, blk], cache_pos)
                             if block_cache is not None:
                                 # the replay wrote every layer's block rows (StaticBlockCache.update)
                                 block_cache._num_initialized = cfg.num_hidden_layers
                         else:
-                            logits = full_fwd(x[:, blk], cache_pos)
-                        logits = torch.cat([logits[:, :1], logits[:, :-1]], dim=1)[:, s0:s1]
+                            raw = full_fwd(x[:, blk], cache_pos)
+                        row_offset = s0
                     stats.forwards += 1
+                    if fused:
+                        # logits shifted by one position (:774): position i reads raw row
+                        # max(row_offset + i - 1, 0)
+                        scratch = ops.unmask_step(raw, x[:, blk.start + s0:blk.start + s1], mask_id, threshold,
+                                                  row_offset=row_offset, shift=1, finished=finished,
+                                                  stop_token=stop_token, scratch=scratch)
+                        n_unmasked, n_left, n_first, n_finished = scratch.counts.tolist()
+                        stats.step_tokens.append(n_unmasked)
+                        left, first_masked = n_left > 0, n_first > 0
+                        if n_finished == B:
+                            break
+                        continue
+                    logits = torch.cat([raw[:, :1], raw[:, :-1]], dim=1)[:, row_offset:row_offset + small_block_size]
                     tok, conf = greedy_with_confidence(logits)
                     m = mask[:, s0:s1] & ~finished[:, None]
                     if policy is None:
@@ -236,6 +256,9 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
                     stats.step_tokens.append(int(unmask.sum()))
                     if bool(finished.all()):
                         break
+                    mask = x[:, blk] == mask_id
+                    left = bool((mask[:, s0:s1] & ~finished[:, None]).any())
+                    first_masked = bool(mask[:, s0].any())
             # ---- commit (generation_functions.py:685-696)
             logits = model(x[:, blk], cache, update_past_key_values=True)
             stats.forwards += 1

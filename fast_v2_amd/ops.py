@@ -371,6 +371,53 @@ def rope_kv_write(
     return (q_out, kv_o) if kv_out else q_out
 
 
+class UnmaskScratch:
+    """Device buffers of one sampler (greedy token and confidence per position, four
+    counters), allocated once per (batch, positions, device)."""
+
+    def __init__(self, batch: int, positions: int, device):
+        self.row_tok = torch.empty((batch, positions), dtype=torch.int64, device=device)
+        self.row_conf = torch.empty((batch, positions), dtype=torch.float32, device=device)
+        self.counts = torch.zeros(4, dtype=torch.int32, device=device)
+
+
+def unmask_step(logits: torch.Tensor, tokens: torch.Tensor, mask_id: int, threshold: float,
+                row_offset: int = 0, shift: int = 1, finished: Optional[torch.Tensor] = None,
+                stop_token: Optional[int] = None, scratch: Optional[UnmaskScratch] = None) -> UnmaskScratch:
+    """Greedy sampling + threshold unmasking of one sub-block step, on the GPU.
+
+    logits [B, R, V] (16-bit, vocab contiguous); position i of the sub-block reads row
+    max(row_offset + i - shift, 0). tokens [B, L] int64 (positions contiguous) is
+    updated in place; finished [B] bool / uint8 (or None) too. Returns the scratch
+    whose ``counts`` = [unmasked, masked left in unfinished rows, rows with position 0
+    still masked, finished rows] and ``row_tok`` / ``row_conf`` hold the greedy token
+    and its probability per position (generation_functions.py:784-807,
+    modeling.py:2263-2270)."""
+    if logits.dim() != 3 or tokens.dim() != 2 or tokens.shape[0] != logits.shape[0]:
+        raise RuntimeError("unmask_step: logits [B, R, V] and tokens [B, L] expected")
+    dev = _require_gpu(logits, tokens, *([finished] if finished is not None else []))
+    if logits.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError("unmask_step: logits must be bf16 or fp16")
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    if tokens.dtype != torch.int64 or tokens.stride(-1) != 1:
+        raise RuntimeError("unmask_step: tokens must be int64 with contiguous positions (updated in place)")
+    B, L = tokens.shape
+    if finished is not None and (finished.dtype not in (torch.bool, torch.uint8) or not finished.is_contiguous()
+                                 or finished.numel() != B):
+        raise RuntimeError("unmask_step: finished must be a contiguous bool / uint8 [B]")
+    if scratch is None or scratch.row_tok.shape != (B, L) or scratch.row_tok.device != dev:
+        scratch = UnmaskScratch(B, L, dev)
+    rc = _ffi.lib().fdllm_unmask_step(
+        logits.data_ptr(), logits.stride(0), logits.stride(1), logits.shape[2], int(row_offset), int(shift),
+        tokens.data_ptr(), tokens.stride(0), _ptr(finished), int(mask_id), float(threshold),
+        -1 if stop_token is None else int(stop_token),
+        scratch.row_tok.data_ptr(), scratch.row_conf.data_ptr(), scratch.counts.data_ptr(),
+        B, L, _ffi.dtype_code(logits.dtype), _ffi.stream_ptr(dev))
+    _ffi.check(rc, "fdllm_unmask_step")
+    return scratch
+
+
 def kv_cache_write(
     k_new: torch.Tensor,
     v_new: torch.Tensor,

@@ -264,6 +264,38 @@ typedef struct fdllm_rope_kv_desc {
 
 int fdllm_rope_kv_write(const fdllm_rope_kv_desc* desc, void* stream);
 
+/* -------------------------------------------------------------------------
+ * One greedy sampling + threshold unmasking step of a sub-block.
+ *
+ *   for b < batch, i < num_positions (<= 64):
+ *     row    = logits[b, max(row_offset + i - shift, 0), :]   (shift 1: the one-
+ *              position shift of the diffusion logits)
+ *     p      = softmax(row), rounded to the logits' dtype
+ *     tok    = first index of max(p);   conf = p[tok]
+ *     row_tok[b, i] = tok;  row_conf[b, i] = conf
+ *     masked = tokens[b, i] == mask_id and not finished[b]
+ *     unmask = masked and (conf > threshold or i is the first position of
+ *              max(conf over masked positions of b))
+ *     if unmask: tokens[b, i] = tok;   finished[b] |= unmask and tok == stop_token
+ *   counts[0] = positions unmasked, counts[1] = masked positions left in rows not
+ *   finished, counts[2] = rows whose position 0 is still masked, counts[3] =
+ *   finished rows (all after the step).
+ *
+ * tokens is int64 with the positions of a row contiguous; finished is a byte per
+ * row or NULL; stop_token < 0 disables the stop rule. row_tok / row_conf are
+ * [batch, num_positions] outputs, counts an int32[4] output. Two kernels on
+ * `stream`; the caller reads counts to decide the next step.
+ *
+ * Replaces: sample_with_top_p at temperature 0 (modeling.py:2263-2270 of the
+ * model snapshot) and the unmask rule of batch_sample_dynamo
+ * (generation_functions.py:784-807).
+ * ------------------------------------------------------------------------- */
+int fdllm_unmask_step(const void* logits, int64_t logits_stride_b, int64_t logits_stride_row, int vocab,
+                      int row_offset, int shift, int64_t* tokens, int64_t tokens_stride_b,
+                      uint8_t* finished, int64_t mask_id, float threshold, int64_t stop_token,
+                      int64_t* row_tok, float* row_conf, int32_t* counts,
+                      int batch, int num_positions, int dtype, void* stream);
+
 #ifdef __cplusplus
 } /* extern "C" */
 #endif
