@@ -265,9 +265,14 @@ def bench_e2e(torch, args):
     from fast_v2_amd.e2e import sampler as es
 
     dev = torch.device("cuda", 0)
-    cfg = em.BlockDiffusionConfig()
     t0 = time.perf_counter()
-    model = em.build_model(cfg, dev)
+    if args.e2e_weights:
+        from fast_v2_amd.e2e import weights as ew
+        model = ew.load_model(args.e2e_weights, dev)
+        cfg = model.config
+    else:
+        cfg = em.BlockDiffusionConfig()
+        model = em.build_model(cfg, dev)
     torch.cuda.synchronize()
     build_s = time.perf_counter() - t0
     g = torch.Generator().manual_seed(0)
@@ -290,7 +295,8 @@ def bench_e2e(torch, args):
            "params": em.param_count(cfg), "model_build_s": round(build_s, 2),
            "gemm_tuning": "torch TunableOp over hipBLASLt / rocBLAS solutions, tuned in the warm-up",
            "forwards_graphed": "diffusion steps replayed from HIP graphs; commits eager",
-           "config": "28 layers, hidden 3584, 28/4 heads, vocab 152064, bf16 random init; batch 16, prompt 512, "
+           "weights": args.e2e_weights or "random init (N(0, 0.02))",
+           "config": "28 layers, hidden 3584, 28/4 heads, vocab 152064, bf16; batch 16, prompt 512, "
                      f"{args.e2e_tokens} new tokens, block 32, sub-block 8, threshold 0.9 (p > 0.9), block cache on"}
     del model, out, x
     torch.cuda.empty_cache()
@@ -335,6 +341,8 @@ def main() -> int:
     ap.add_argument("--only", choices=["decode", "gather", "prefill", "e2e"], default=None)
     ap.add_argument("--e2e-tokens", type=int, default=1024, help="tokens generated in the end-to-end leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end generation leg")
+    ap.add_argument("--e2e-weights", default=None,
+                    help="local checkpoint directory (config.json + *.safetensors) instead of random weights")
     ap.add_argument("--calibrate", action="store_true",
                     help="also time plain device copies of the workloads' sizes (practical bandwidth floor)")
     ap.add_argument("--copy-calibration", action="store_true",
