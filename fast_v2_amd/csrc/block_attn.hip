@@ -774,7 +774,7 @@ __device__ __forceinline__ int active_splits(int t, int n) {
   return ceil_div_small(t, ceil_div_small(t, n));
 }
 
-// Partition of every sequence's keys into splits of equal size (whole 32-key tiles).
+// Partition of every sequence's keys into splits of equal size (whole TILE-key tiles).
 //   * Fixed (chunk > 0, grid (n_splits, Hkv, B)): sequence b gets
 //     n = ceil(tiles / chunk tiles) splits, capped at kMaxDecodeSplits.
 //   * Balanced (chunk == 0, B <= 64, grid (S, Hkv, 1)): sequence b gets
@@ -785,15 +785,15 @@ __device__ __forceinline__ int active_splits(int t, int n) {
 //     chunk gives the short sequences half-empty workgroups. Every workgroup
 //     evaluates the same integer search (binary, on one wave's lanes, one lane per
 //     sequence), so all of them agree on the partition.
-template <bool PAGED>
+template <bool PAGED, int TILE = 32>
 __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
   DecodePart dp;
   if (p.chunk > 0) {
     dp.b = blockIdx.z;
     dp.split = blockIdx.x;
     const SeqInfo si = seq_info<PAGED>(p, dp.b, 0);
-    const int t = (si.kv_end + 31) >> 5;
-    const int ct = p.chunk >> 5;
+    const int t = (si.kv_end + TILE - 1) / TILE;
+    const int ct = p.chunk / TILE;
     const int n = max(1, min(kMaxDecodeSplits, (t + ct - 1) / ct));
     const int size = (t + n - 1) / n;
     dp.n_act = active_splits(t, n);
@@ -801,8 +801,8 @@ __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
     dp.seqlen = si.seqlen;
     dp.qs = si.qs;
     dp.kv_end = si.kv_end;
-    dp.k_lo = dp.split * size * 32;
-    dp.k_hi = min(si.kv_end, dp.k_lo + size * 32);
+    dp.k_lo = dp.split * size * TILE;
+    dp.k_hi = min(si.kv_end, dp.k_lo + size * TILE);
     if (dp.split >= dp.n_act) dp.b = -1;
     return dp;
   }
@@ -811,7 +811,7 @@ __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
   SeqInfo sl;
   sl.seqlen = sl.qs = sl.kv_end = 0;
   if (has) sl = seq_info<PAGED>(p, lane, 0);
-  const int t = (sl.kv_end + 31) >> 5;
+  const int t = (sl.kv_end + TILE - 1) / TILE;
   const int S = p.n_splits;
   // splits of a sequence for C tiles per split (an empty sequence still takes one
   // slot); the count over-estimates only where the cap of kMaxDecodeSplits bites
@@ -848,8 +848,8 @@ __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
   dp.qs = __builtin_amdgcn_readlane(sl.qs, b);
   dp.kv_end = __builtin_amdgcn_readlane(sl.kv_end, b);
   const int size = __builtin_amdgcn_readlane(size_l, b);
-  dp.k_lo = dp.split * size * 32;
-  dp.k_hi = min(dp.kv_end, dp.k_lo + size * 32);
+  dp.k_lo = dp.split * size * TILE;
+  dp.k_hi = min(dp.kv_end, dp.k_lo + size * TILE);
   return dp;
 }
 
@@ -858,13 +858,13 @@ __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
 // 64-row worst case takes one pass of 512 threads; the splits are folded in
 // groups of eight whose loads are all issued before any is used (one memory
 // round trip up to eight splits), with the running maximum moved between groups.
-template <bool F16>
+template <bool F16, int RS = 64>  // RS: partial rows per slot
 __device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh, int64_t slot0, int n_act, int tid,
                                              int nthreads) {
   constexpr int D = 128;
   constexpr int GS = 8;
-  const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot0 * 64 * D, 0, n_act * 64 * D * 4, kBufferFlags);
-  const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot0 * 64, 0, n_act * 64 * 8, kBufferFlags);
+  const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot0 * RS * D, 0, n_act * RS * D * 4, kBufferFlags);
+  const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot0 * RS, 0, n_act * RS * 8, kBufferFlags);
   for (int item = tid; item < p.R * 8; item += nthreads) {
     // columns 4 c8 + 32 j + (0..3), j = 0..3: the eight threads of a row read 128
     // contiguous bytes per load
@@ -880,7 +880,7 @@ __device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh
 #pragma unroll
       for (int u = 0; u < GS; ++u) {
         // splits past n_act read as zero (outside the descriptor) and weigh nothing
-        const int row = (s0 + u) * 64 + r;
+        const int row = (s0 + u) * RS + r;
         ml[u] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(mrsrc, row * 8, 0, kSc1));
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -1306,7 +1306,7 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, c
 //     start first; workgroup ids of one (sequence, KV head) differ by a multiple
 //     of B * Hkv, which keeps its row blocks on one XCD (and its K/V in one L2)
 //     when B * Hkv is a multiple of 8.
-template <bool F16, bool PAGED>
+template <bool F16, bool PAGED, bool SPLIT>
 __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) {
   constexpr int D = 128;
   constexpr int KT = 64;
@@ -1324,14 +1324,37 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
   const int l16 = lane & 15;
   const int g16 = lane >> 4;
 
-  const int unit = blockIdx.x;
-  const int b = unit / p.Hkv;
-  const int kvh = unit - b * p.Hkv;
-  const int rb = p.n_rb - 1 - static_cast<int>(blockIdx.y);
-  const SeqInfo si = seq_info<PAGED>(p, b, rb);
+  int b, kvh, rb, k_lo, k_hi, n_act, split, first;
+  SeqInfo si;
+  if constexpr (SPLIT) {
+    // one row block of at most 256 rows per (sequence, KV head); keys split as in the
+    // split decode kernel, in 64-key tiles
+    kvh = blockIdx.y;
+    const DecodePart dp = decode_partition<PAGED, KT>(p);
+    if (dp.b < 0) return;  // idle slot (uniform over the workgroup)
+    b = __builtin_amdgcn_readfirstlane(dp.b);
+    split = __builtin_amdgcn_readfirstlane(dp.split);
+    n_act = __builtin_amdgcn_readfirstlane(dp.n_act);
+    first = __builtin_amdgcn_readfirstlane(dp.first);
+    k_lo = __builtin_amdgcn_readfirstlane(dp.k_lo);
+    k_hi = __builtin_amdgcn_readfirstlane(dp.k_hi);
+    rb = 0;
+    si.seqlen = dp.seqlen;
+    si.qs = dp.qs;
+    si.kv_end = dp.kv_end;
+  } else {
+    const int unit = blockIdx.x;
+    b = unit / p.Hkv;
+    kvh = unit - b * p.Hkv;
+    rb = p.n_rb - 1 - static_cast<int>(blockIdx.y);
+    si = seq_info<PAGED>(p, b, rb);
+    k_lo = 0;
+    k_hi = si.kv_end;
+    n_act = 1;
+    split = first = 0;
+  }
   const int row0 = rb * 256;
-  const int kv_end = si.kv_end;
-  const int ntiles = (kv_end + KT - 1) / KT;
+  const int ntiles = k_hi > k_lo ? (k_hi - k_lo + KT - 1) / KT : 0;
 
   // ---- this lane's query row: Q^T fragments and key limit
   const int r = row0 + wave * 32 + n32;
@@ -1378,8 +1401,32 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
   Stage st0, st1;
 
   auto load_tile = [&](Stage& sg, int j) {
-    const int kb = j * KT;
-    const int valid = __builtin_amdgcn_readfirstlane(max(0, min(KT, kv_end - kb)));
+    const int kb = k_lo + j * KT;
+    if constexpr (PAGED) {
+      if (p.page_size < KT) {
+        // 32-key pages: chunk i of every thread lies in key half i of the tile
+        // (rows tid / 16 + 32 i), each half on its own page
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          const int kh = kb + 32 * i;
+          const int valid = __builtin_amdgcn_readfirstlane(max(0, min(32, k_hi - kh)));
+          const int page = pt_row[min(kh >> p.page_shift, p.max_pages - 1)];
+          const int slot0 = kh & (p.page_size - 1);
+          const int64_t koffs = static_cast<int64_t>(page) * p.k_sp + slot0 * p.k_ss;
+          const int64_t voffs = static_cast<int64_t>(page) * p.v_sp + slot0 * p.v_ss;
+          const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase + koffs), 0,
+                                                                              valid * krow_bytes, kBufferFlags);
+          const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase + voffs), 0,
+                                                                              valid * vrow_bytes, kBufferFlags);
+          sg.k[i] = __builtin_bit_cast(u32x4,
+                                       __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i] - 32 * i * krow_bytes, 0, 0));
+          sg.v[i] = __builtin_bit_cast(u32x4,
+                                       __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i] - 32 * i * vrow_bytes, 0, 0));
+        }
+        return;
+      }
+    }
+    const int valid = __builtin_amdgcn_readfirstlane(max(0, min(KT, k_hi - kb)));
     int64_t koffs, voffs;
     if constexpr (PAGED) {
       // page_size >= 64 and tiles start at multiples of 64: one page per tile
@@ -1483,7 +1530,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
     store_tile(sg, j & 1);
     lds_barrier();
     load_tile(sg, j + 2);
-    const int kb = j * KT;
+    const int kb = k_lo + j * KT;
     if (j < ntiles && kb < lim_max) compute_tile(j & 1, kb);  // wave-uniform
   };
   if (ntiles > 0) {
@@ -1497,6 +1544,38 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
 
   // ---- epilogue: rows of both lane halves are whole after the exchange of l
   l_run = halves_sum(l_run);
+  if (SPLIT && n_act > 1) {
+    // partial (O, m, l) of this key range: slot rows = the workgroup's 256 rows
+    const int unit = b * p.Hkv + kvh;
+    const int64_t slot0 = first;
+    if (r < p.R) {
+      const int64_t slot = slot0 + split;
+      const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot * 256 * D, 0, 256 * D * 4, kBufferFlags);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, f32x4{acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]}),
+              orsrc, (r * D + 32 * dt + 8 * i + 4 * h) * 4, 0, kSc1);
+      if (h == 0) {
+        const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot * 256, 0, 256 * 8, kBufferFlags);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)), mrsrc, r * 8, 0,
+                                              kSc1);
+      }
+    }
+    // last workgroup of the unit merges (the protocol of kv_split_decode_kernel)
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    __shared__ int s_last;
+    if (tid == 0)
+      s_last = __hip_atomic_fetch_add(&p.ws_cnt[unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_act - 1;
+    __syncthreads();
+    if (!s_last) return;
+    merge_splits<F16, 256>(p, b, kvh, slot0, n_act, tid, 512);
+    if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return;
+  }
   if (r < p.R) {
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
     uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh;
@@ -1629,7 +1708,7 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const KVWriteArgs a) {
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Kernel families a call can take (make_plan picks one per descriptor).
-enum PlanKind { kPlanGeneral = 0, kPlanAllHeads = 1, kPlanSplitDecode = 2, kPlanPrefill = 3 };
+enum PlanKind { kPlanGeneral = 0, kPlanAllHeads = 1, kPlanSplitDecode = 2, kPlanPrefill = 3, kPlanSplitPrefill = 4 };
 
 struct Plan {
   int kind;     // PlanKind
@@ -1752,10 +1831,57 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
     }
     return FDLLM_OK;
   }
-  // Prefill shapes: at least 8 row blocks of 256 per KV head, pages of >= 64 keys
+  // Block decode shapes (64 < rows per KV head <= 256, e.g. a whole 32-token block at
+  // GQA 7): the prefill kernel's math on one row block, keys split and merged as in the
+  // split decode kernel (64-key tiles)
+  const bool split_prefill_shape = !(d->flags & FDLLM_ATTN_NO_DECODE_KERNEL) && d->head_dim == 128 &&
+                                   pl->R > 64 && pl->R <= 256 && (d->kv_split == 0 || d->kv_split % 64 == 0) &&
+                                   (d->page_table == nullptr || d->page_size >= 32) &&
+                                   d->k_stride_slot < (1 << 24) && d->v_stride_slot < (1 << 24);
+  if (split_prefill_shape) {
+    const int max_len = d->page_table
+                            ? std::min<int64_t>(d->max_seqlen, static_cast<int64_t>(d->max_pages) * d->page_size)
+                            : d->max_seqlen;
+    const int64_t max_t = (std::max(1, max_len) + 63) / 64;  // 64-key tiles of the longest sequence
+    if (max_t <= static_cast<int64_t>(kDecodeMaxTiles) * kMaxDecodeSplits &&
+        static_cast<int64_t>(d->batch) * hkv <= static_cast<int64_t>(kCounterBytes / sizeof(int))) {
+      const int64_t B = std::max(d->batch, 1);
+      const int64_t min_splits = (max_t + kDecodeMaxTiles - 1) / kDecodeMaxTiles;
+      pl->kind = kPlanSplitPrefill;
+      pl->decode = false;
+      pl->MT = 4;
+      pl->rows_per_wg = 256;
+      pl->n_rb = 1;
+      int64_t slots;
+      bool split_possible;
+      if (d->kv_split == 0 && B <= kBalancedMaxBatch) {
+        pl->chunk = 0;
+        slots = std::max<int64_t>((kSplitTargetWG + hkv - 1) / hkv, B * min_splits);
+        pl->n_splits = static_cast<int>(slots);
+        split_possible = slots > B;
+      } else {
+        int64_t chunk = d->kv_split > 0 ? d->kv_split : static_cast<int64_t>(kDecodeMaxTiles) * 64;
+        chunk = std::max<int64_t>(chunk, (max_t + kMaxDecodeSplits - 1) / kMaxDecodeSplits * 64);
+        chunk = std::min<int64_t>(chunk, static_cast<int64_t>(kDecodeMaxTiles) * 64);
+        pl->chunk = static_cast<int>(chunk);
+        pl->n_splits = static_cast<int>((max_t * 64 + chunk - 1) / chunk);
+        slots = B * pl->n_splits;
+        split_possible = pl->n_splits > 1;
+      }
+      FDLLM_CHECK_ARG(slots * hkv < (int64_t{1} << 31) / 256, "fdllm_kv_attn: too many split slots");
+      if (split_possible) {
+        pl->ws_o_bytes = static_cast<size_t>(slots) * hkv * 256 * d->head_dim * sizeof(float);
+        pl->ws_ml_bytes = static_cast<size_t>(slots) * hkv * 256 * sizeof(float2);
+      } else {
+        pl->ws_o_bytes = pl->ws_ml_bytes = 0;
+      }
+      return FDLLM_OK;
+    }
+  }
+  // Prefill shapes: at least 8 row blocks of 256 per KV head, pages of >= 32 keys
   const bool prefill_shape = !(d->flags & FDLLM_ATTN_NO_DECODE_KERNEL) && d->head_dim == 128 &&
                              pl->R >= 8 * 256 && d->kv_split == 0 &&
-                             (d->page_table == nullptr || d->page_size >= 64) && d->k_stride_slot < (1 << 24) &&
+                             (d->page_table == nullptr || d->page_size >= 32) && d->k_stride_slot < (1 << 24) &&
                              d->v_stride_slot < (1 << 24) && (pl->R + 255) / 256 < 65536;
   if (prefill_shape) {
     pl->kind = kPlanPrefill;
@@ -1973,11 +2099,23 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
     const bool paged = p.page_table != nullptr;
     const dim3 grid(static_cast<unsigned>(grid_z), pl.n_rb);
     if (f16) {
-      if (paged) kv_prefill_kernel<true, true><<<grid, dim3(512), 0, s>>>(p);
-      else kv_prefill_kernel<true, false><<<grid, dim3(512), 0, s>>>(p);
+      if (paged) kv_prefill_kernel<true, true, false><<<grid, dim3(512), 0, s>>>(p);
+      else kv_prefill_kernel<true, false, false><<<grid, dim3(512), 0, s>>>(p);
     } else {
-      if (paged) kv_prefill_kernel<false, true><<<grid, dim3(512), 0, s>>>(p);
-      else kv_prefill_kernel<false, false><<<grid, dim3(512), 0, s>>>(p);
+      if (paged) kv_prefill_kernel<false, true, false><<<grid, dim3(512), 0, s>>>(p);
+      else kv_prefill_kernel<false, false, false><<<grid, dim3(512), 0, s>>>(p);
+    }
+    FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
+  }
+  if (pl.kind == kPlanSplitPrefill) {
+    const bool paged = p.page_table != nullptr;
+    const dim3 grid(pl.n_splits, d->num_kv_heads, pl.chunk > 0 ? d->batch : 1);
+    if (f16) {
+      if (paged) kv_prefill_kernel<true, true, true><<<grid, dim3(512), 0, s>>>(p);
+      else kv_prefill_kernel<true, false, true><<<grid, dim3(512), 0, s>>>(p);
+    } else {
+      if (paged) kv_prefill_kernel<false, true, true><<<grid, dim3(512), 0, s>>>(p);
+      else kv_prefill_kernel<false, false, true><<<grid, dim3(512), 0, s>>>(p);
     }
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }

@@ -375,7 +375,8 @@ def _paginate(k, v, page_size, g):
 @pytest.mark.parametrize("case", [
     "gqa7_block_causal_prefix",   # 28/4 heads, cached prefix + new rows, block-causal
     "gqa7_fp16_paged64",          # the same in fp16 over 64-key pages
-    "gqa7_paged32",               # 32-key pages: the general kernel takes the call
+    "gqa7_paged32",               # 32-key pages: two pages per 64-key tile
+    "gqa7_paged16",               # 16-key pages: the general kernel takes the call
     "mha_causal_paged256",        # 8/8 heads (G = 1), causal, 256-key pages
     "gqa8_full_ragged",           # 16/2 heads, every key visible, ragged lengths
     "gqa4_block64_one_head",      # 4/1 heads, 64-key blocks
@@ -392,6 +393,8 @@ def test_prefill_kernel(gpu, case):
         B, Sq, hq, hkv, lens, dtype, page = 2, 300, 28, 4, [812, 333], torch.float16, 64
     elif case == "gqa7_paged32":
         B, Sq, hq, hkv, lens, page = 2, 300, 28, 4, [700, 333], 32
+    elif case == "gqa7_paged16":
+        B, Sq, hq, hkv, lens, page = 2, 300, 28, 4, [700, 333], 16
     elif case == "mha_causal_paged256":
         B, Sq, hq, hkv, lens, mode, page = 1, 2100, 8, 8, [2400], _ffi.MASK_CAUSAL, 256
     elif case == "gqa8_full_ragged":
@@ -413,4 +416,43 @@ def test_prefill_kernel(gpu, case):
     for prefill in (True, False):  # False: the general kernel on the same call
         out = ops.block_attn(q.to(gpu), kc.to(gpu), vc.to(gpu), sl.to(gpu), mask_mode=mode, mask_block=blk,
                              decode_kernel=prefill, **args)
+        _check(out, exp)
+
+
+@pytest.mark.parametrize("case", ["bs16_paged32", "ragged_contig", "fp16_paged64", "fixed_chunks", "gqa8_256_rows"])
+def test_block_decode_split_prefill_kernel(gpu, case):
+    """A whole 32-token block per step (64 < rows per KV head <= 256): the prefill
+    kernel's math with split keys and the in-kernel merge, against the oracle and
+    against the general kernel on the same call."""
+    split, dtype, decode_args = 0, torch.bfloat16, {}
+    if case == "bs16_paged32":
+        wl = workloads.kv_decode_paged(seed=0, active=32)
+    elif case == "fp16_paged64":
+        wl = workloads.kv_decode_paged(seed=3, batch=6, active=32, page_size=64, dtype=torch.float16)
+    elif case == "fixed_chunks":
+        wl = workloads.kv_decode_paged(seed=4, batch=5, active=32)
+        split = 128
+    elif case == "gqa8_256_rows":
+        wl = workloads.kv_decode_paged(seed=5, batch=3, num_q_heads=16, num_kv_heads=2, active=32)
+    else:
+        wl = None
+    if wl is not None:
+        q, kc, vc, sl = wl.q, wl.k_pool, wl.v_pool, wl.seqlens
+        args = dict(page_table=wl.page_table.to(gpu), page_size=wl.page_size)
+        exp = oa.attention_np(q.float(), kc.float(), vc.float(), sl, wl.scale, page_table=wl.page_table,
+                              page_size=wl.page_size)
+        scale = wl.scale
+    else:
+        g = torch.Generator().manual_seed(12)
+        B, Sq, Hq, Hkv, D, S = 5, 32, 28, 4, 128, 3000
+        q = torch.randn(B, Sq, Hq, D, generator=g).to(dtype)
+        kc = torch.randn(B, S, Hkv, D, generator=g).to(dtype)
+        vc = torch.randn(B, S, Hkv, D, generator=g).to(dtype)
+        sl = torch.tensor([3000, 0, 1, 97, 2048], dtype=torch.int32)
+        args, scale = {}, None
+        exp = oa.attention_np(q.float(), kc.float(), vc.float(), sl)
+    print(f"case block decode {case}", flush=True)
+    for dk in (True, False):
+        out = ops.block_attn(q.to(gpu), kc.to(gpu), vc.to(gpu), sl.to(gpu), scale, kv_split=split,
+                             decode_kernel=dk, **args)
         _check(out, exp)
