@@ -198,7 +198,9 @@ def bench_gather(torch, args):
 
     dev = torch.device("cuda", 0)
     wl = workloads.gather_rmsnorm_rows(seed=0)
-    copies = 16  # 16 x 29 MB of hidden states: larger than the last-level cache
+    # 48 copies of the 29 MB hidden states: the rows one cycle touches (48 x 7.3 MB) exceed
+    # the 256 MB last-level cache, so every call reads its rows from HBM
+    copies = 48
     hs = [wl.hidden.to(dev)]
     for _ in range(copies - 1):
         hs.append(hs[0].clone())

@@ -130,6 +130,14 @@ __device__ __forceinline__ float apply_norm(float x, float inv, float w, int mod
   return w * Vec16<T>::round(x * inv);
 }
 
+// Compile-time form of apply_norm for the vector path. NORM_PLAIN is the fp32 form with
+// a weight of 1 (x * inv * 1 == x * inv exactly).
+template <typename T, bool CAST>
+__device__ __forceinline__ float apply_norm_ct(float x, float inv, float w) {
+  if constexpr (CAST) return w * Vec16<T>::round(x * inv);
+  return (x * inv) * w;
+}
+
 struct GatherArgs {
   const void* hidden;
   int64_t hs_b, hs_s;
@@ -145,20 +153,23 @@ struct GatherArgs {
 };
 
 // Vector path: H * sizeof(T) is a multiple of 16 and every row is 16-byte aligned.
-// VPL = 16-byte vectors per lane (the whole row stays in registers).
-template <typename T, int WK, int VPL>
+// VPL = 16-byte vectors per lane (the whole row stays in registers). The norm form is a
+// template parameter, so the per-element code is straight-line. Outputs are written once
+// and not read again by this kernel: non-temporal (streaming) stores.
+template <typename T, int WK, bool CAST, int VPL>
 __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArgs a) {
   constexpr int N = Vec16<T>::N;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= static_cast<int64_t>(a.B) * a.T) return;
-  const int b = static_cast<int>(row / a.T);
-  const int t = static_cast<int>(row - static_cast<int64_t>(b) * a.T);
+  const int row = static_cast<int>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // B * T < 2^31 (host check)
+  if (row >= a.B * a.T) return;
+  const int b = row / a.T;
+  const int t = row - b * a.T;
   const int nvec = a.H / N;
   const int64_t src = a.idx[b * a.is_b + t];
 
-  u32x4* nrow = reinterpret_cast<u32x4*>(static_cast<T*>(a.normed) + row * a.H);
-  u32x4* grow = a.gathered ? reinterpret_cast<u32x4*>(static_cast<T*>(a.gathered) + row * a.H) : nullptr;
+  u32x4* nrow = reinterpret_cast<u32x4*>(static_cast<T*>(a.normed) + static_cast<int64_t>(row) * a.H);
+  u32x4* grow = a.gathered ? reinterpret_cast<u32x4*>(static_cast<T*>(a.gathered) + static_cast<int64_t>(row) * a.H)
+                           : nullptr;
 
   if (src < 0 || src >= a.S) {
     const u32x4 z = {0u, 0u, 0u, 0u};
@@ -166,27 +177,28 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
     for (int v = 0; v < VPL; ++v) {
       const int c = lane + kWave * v;
       if (c < nvec) {
-        nrow[c] = z;
-        if (grow) grow[c] = z;
+        __builtin_nontemporal_store(z, nrow + c);
+        if (grow) __builtin_nontemporal_store(z, grow + c);
       }
     }
     return;
   }
 
   const u32x4* hrow = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.hidden) + b * a.hs_b + src * a.hs_s);
-  // All loads are issued unconditionally (clamped index) and back to back, so the
-  // whole row is in flight at once; lanes past the row end are zeroed afterwards.
+  // All loads are issued unconditionally and back to back, so the whole row is in flight
+  // at once. nvec lies in (64 (VPL - 1), 64 VPL], so only the last vector can run past the
+  // row end: its index is clamped and its lanes past the end are zeroed afterwards.
+  const int clast = lane + kWave * (VPL - 1);
+  const bool last_in = clast < nvec;
   u32x4 x[VPL];
 #pragma unroll
-  for (int v = 0; v < VPL; ++v) x[v] = hrow[min(lane + kWave * v, nvec - 1)];
+  for (int v = 0; v < VPL - 1; ++v) x[v] = hrow[lane + kWave * v];
+  x[VPL - 1] = hrow[last_in ? clast : nvec - 1];
   float w[VPL][N];
 #pragma unroll
-  for (int v = 0; v < VPL; ++v) load_weight<T, WK, N>(a.weight, min(lane + kWave * v, nvec - 1) * N, w[v]);
-  if (nvec % kWave != 0) {
-#pragma unroll
-    for (int v = 0; v < VPL; ++v)
-      if (lane + kWave * v >= nvec) x[v] = u32x4{0u, 0u, 0u, 0u};
-  }
+  for (int v = 0; v < VPL - 1; ++v) load_weight<T, WK, N>(a.weight, (lane + kWave * v) * N, w[v]);
+  load_weight<T, WK, N>(a.weight, (last_in ? clast : nvec - 1) * N, w[VPL - 1]);
+  if (!last_in) x[VPL - 1] = u32x4{0u, 0u, 0u, 0u};
 
   float ss = 0.f;
 #pragma unroll
@@ -201,15 +213,15 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
 
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
-    const int c = lane + kWave * v;
     float f[N];
     Vec16<T>::unpack(x[v], f);
 #pragma unroll
-    for (int i = 0; i < N; ++i) f[i] = apply_norm<T>(f[i], inv, w[v][i], a.mode);
+    for (int i = 0; i < N; ++i) f[i] = apply_norm_ct<T, CAST>(f[i], inv, w[v][i]);
     const u32x4 o = Vec16<T>::pack(f);
-    if (c < nvec) {
-      if (grow) grow[c] = x[v];
-      nrow[c] = o;
+    if (v < VPL - 1 || last_in) {
+      const int c = lane + kWave * v;
+      if (grow) __builtin_nontemporal_store(x[v], grow + c);
+      __builtin_nontemporal_store(o, nrow + c);
     }
   }
 }
@@ -316,14 +328,14 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(const ScatterArgs a) 
   }
 }
 
-template <typename T, int WK>
+template <typename T, int WK, bool CAST>
 bool launch_gather_vec(const GatherArgs& a, dim3 grid, hipStream_t stream) {
   const int nvec = a.H / Vec16<T>::N;
   const int vpl = (nvec + kWave - 1) / kWave;
   switch (vpl) {
-#define FDLLM_VPL_CASE(n)                                                  \
-  case n:                                                                  \
-    gather_rmsnorm_vec_kernel<T, WK, n><<<grid, dim3(256), 0, stream>>>(a); \
+#define FDLLM_VPL_CASE(n)                                                        \
+  case n:                                                                        \
+    gather_rmsnorm_vec_kernel<T, WK, CAST, n><<<grid, dim3(256), 0, stream>>>(a); \
     return true;
     FDLLM_VPL_CASE(1)
     FDLLM_VPL_CASE(2)
@@ -343,6 +355,12 @@ bool launch_gather_vec(const GatherArgs& a, dim3 grid, hipStream_t stream) {
   }
 }
 
+template <typename T, int WK>
+bool launch_gather_vec_mode(const GatherArgs& a, dim3 grid, hipStream_t stream) {
+  return a.mode == FDLLM_NORM_WEIGHT_AFTER_CAST ? launch_gather_vec<T, WK, true>(a, grid, stream)
+                                                : launch_gather_vec<T, WK, false>(a, grid, stream);
+}
+
 template <typename T>
 int launch_gather(const GatherArgs& a, bool vec, hipStream_t stream) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.T;
@@ -350,13 +368,13 @@ int launch_gather(const GatherArgs& a, bool vec, hipStream_t stream) {
   if (vec) {
     bool done;
     if (a.mode == FDLLM_NORM_PLAIN) {
-      done = launch_gather_vec<T, kWNone>(a, grid, stream);
+      done = launch_gather_vec<T, kWNone, false>(a, grid, stream);
     } else if (a.wdtype == FDLLM_DTYPE_F32) {
-      done = launch_gather_vec<T, kW32>(a, grid, stream);
+      done = launch_gather_vec_mode<T, kW32>(a, grid, stream);
     } else if constexpr (!std::is_same<T, float>::value) {
       // 16-bit weights in the rows' own format; other combinations take the generic path
       const bool same = (a.wdtype == FDLLM_DTYPE_BF16) == std::is_same<T, bf16_t>::value;
-      done = same && launch_gather_vec<T, kW16>(a, grid, stream);
+      done = same && launch_gather_vec_mode<T, kW16>(a, grid, stream);
     } else {
       done = false;
     }
@@ -411,6 +429,8 @@ extern "C" int fdllm_gather_rmsnorm(const void* hidden, int64_t hidden_batch_str
   FDLLM_CHECK_ARG(batch >= 0 && seq_len >= 0 && num_tokens >= 0 && hidden_size > 0,
                   "fdllm_gather_rmsnorm: bad sizes B=%d S=%d T=%d H=%d", batch, seq_len, num_tokens, hidden_size);
   if (static_cast<int64_t>(batch) * num_tokens == 0) return FDLLM_OK;
+  FDLLM_CHECK_ARG(static_cast<int64_t>(batch) * num_tokens <= INT32_MAX - 3,
+                  "fdllm_gather_rmsnorm: B * T = %lld rows exceeds 2^31 - 4", static_cast<long long>(batch) * num_tokens);
   FDLLM_CHECK_ARG(hidden && indices && normed, "fdllm_gather_rmsnorm: null pointer");
   FDLLM_CHECK_ARG(norm_mode == FDLLM_NORM_PLAIN || weight != nullptr,
                   "fdllm_gather_rmsnorm: norm_mode %d needs a weight", norm_mode);
