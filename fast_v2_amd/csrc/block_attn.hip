@@ -1462,15 +1462,30 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
     const uint16_t* sk = sKV[buf];
     const uint16_t* sv = sk + KBUF;
     f32x16 s[2];
+    {
+      // the 16 K fragments are read ahead of their products: four reads first, then
+      // one read per product, so each read has three products' time to land
+      u32x4 kf[8][2];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) {
+      for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) s[st][e] = 0.f;
+        for (int st = 0; st < 2; ++st)
+          kf[ks][st] = *reinterpret_cast<const u32x4*>(&sk[(32 * st + n32) * KS + 16 * ks + 8 * h]);
 #pragma unroll
-      for (int ks = 0; ks < 8; ++ks) {
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(&sk[(32 * st + n32) * KS + 16 * ks + 8 * h]);
-        s[st] = mfma32x32x16<F16>(kf, qf[ks], s[st]);
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[st][e] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) s[st] = mfma32x32x16<F16>(kf[ks][st], qf[ks], s[st]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+#pragma unroll
+      for (int i = 0; i < 12; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
       }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
     }
     if (!(kb + KT <= lim_min)) {  // wave-uniform: some row of the wave sees part of the tile
 #pragma unroll
