@@ -15,9 +15,10 @@ region, bracketed by torch.cuda.synchronize(); HIP events recorded on the same
 stream give the per-step time, i.e. the average kernel duration plus the
 inter-kernel gap.
 
-Also reported (same run, under "extra"): gather + RMSNorm (bf16 [4096 x 3584],
-1024 rows) and block-causal prefill with its KV-cache write (4 x 4096 tokens),
-each with its own roofline.
+Also reported (same run, under "extra"): the same step with all 32 block queries
+active (the full-block forward), gather + RMSNorm (bf16 [4096 x 3584], 1024 rows) and
+block-causal prefill with its KV-cache write (4 x 4096 tokens), each with its own
+roofline.
 
 cpu_baseline: the reference's CPU path for the same workload, the SDPA shim of
 tests/test_focus.py:205-228 (oracle.attention.sdpa_kvcache), on the host cores.
@@ -160,6 +161,49 @@ def bench_decode(torch, args):
     return res, wl
 
 
+def bench_decode_full(torch, args):
+    """The same 16 sequences with all 32 block queries active (the full-block forward of a
+    diffusion step): 224 query rows per KV head, run on the prefill kernel's 32x32 MFMA
+    tiles with key splits and the in-kernel merge. Same KV pools and page table layout as
+    the headline step, N(0, 1) on the device."""
+    from fast_v2_amd import ops, workloads
+
+    dev = torch.device("cuda", 0)
+    wl = workloads.kv_decode_paged(seed=0, active=32)
+    layers = args.layers
+    gen = torch.Generator(device=dev).manual_seed(1)
+    kp = torch.empty((layers,) + tuple(wl.k_pool.shape), dtype=wl.k_pool.dtype, device=dev)
+    vp = torch.empty_like(kp)
+    kp.normal_(generator=gen)
+    vp.normal_(generator=gen)
+    q = wl.q.to(dev)
+    pt = wl.page_table.to(dev)
+    sl = wl.seqlens.to(dev)
+    out = torch.empty_like(q)
+    B, Sq, Hq, D = q.shape
+    Hkv = kp.shape[-2]
+
+    def step(i):
+        ops.block_attn(q, kp[i % layers], vp[i % layers], sl, wl.scale, page_table=pt,
+                       page_size=wl.page_size, out=out)
+
+    us = _time_graph(torch, step, args.steps, args.warmup)
+    nbytes = workloads.decode_bytes(wl.seqlens, Hq, Hkv, D, Sq)
+    flops = workloads.decode_flops(wl.seqlens, Hq, D, Sq)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    res = {
+        "us_per_step": us,
+        "bytes_per_step": nbytes,
+        "flops_per_step": flops,
+        "achieved_gbs": gbs,
+        "tflops": flops / (us * 1e-6) / 1e12,
+        "roofline": _roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s", _traffic("kv_attn_decode_full_bs16")),
+    }
+    del q, kp, vp, pt, sl, out
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline_decode(torch, wl, seconds: float):
     """Reference CPU path (SDPA shim) on the same bs16 inputs, bf16, contiguous static cache."""
     from oracle import attention as oa
@@ -286,9 +330,21 @@ def bench_e2e(torch, args):
     tun.enable(True)
     tun.tuning_enable(True)
     tun.set_filename(os.path.join(tempfile.gettempdir(), f"fdllm_tunableop_{os.getpid()}_%d.csv"))
-    es.generate(model, x, max_new_tokens=64, use_block_cache=True)  # warm-up (and GEMM tuning)
+    _log(f"e2e: model built in {build_s:.1f} s; warm-up with GEMM tuning")
+    last = [time.perf_counter()]
+
+    def progress(stats, phase):
+        # one line at most every 20 s, written when a forward has been issued
+        now = time.perf_counter()
+        if now - last[0] >= 20.0:
+            last[0] = now
+            _log(f"e2e {phase}: {stats.forwards} forwards, {stats.commits} commits")
+    es.generate(model, x, max_new_tokens=64, use_block_cache=True,
+                progress=lambda st_: progress(st_, "warm-up"))  # warm-up (and GEMM tuning)
     tun.tuning_enable(False)
-    out, st = es.generate(model, x, max_new_tokens=args.e2e_tokens, use_block_cache=True)
+    _log("e2e: timed generation")
+    out, st = es.generate(model, x, max_new_tokens=args.e2e_tokens, use_block_cache=True,
+                          progress=lambda st_: progress(st_, "timed run"))
     tun.enable(False)
     res = {"tokens_per_s": round(st.tokens_per_second, 1), "generated_tokens": st.generated_tokens,
            "seconds": round(st.seconds, 3), "forwards": st.forwards, "commits": st.commits,
@@ -340,7 +396,7 @@ def main() -> int:
     ap.add_argument("--no-check", action="store_true", help="skip the graph-vs-eager equality check")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["decode", "gather", "prefill", "e2e"], default=None)
+    ap.add_argument("--only", choices=["decode", "decode_full", "gather", "prefill", "e2e"], default=None)
     ap.add_argument("--e2e-tokens", type=int, default=1024, help="tokens generated in the end-to-end leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end generation leg")
     ap.add_argument("--e2e-weights", default=None,
@@ -383,6 +439,10 @@ def main() -> int:
     if args.only in (None, "decode"):
         decode, wl = bench_decode(torch, args)
         _log(f"decode: {decode['us_per_step']:.2f} us/step, {decode['achieved_gbs']:.0f} GB/s")
+    if args.only in (None, "decode_full"):
+        extra["block_decode_full"] = bench_decode_full(torch, args)
+        _log(f"full-block decode: {extra['block_decode_full']['us_per_step']:.2f} us/step, "
+             f"{extra['block_decode_full']['achieved_gbs']:.0f} GB/s, {extra['block_decode_full']['tflops']:.0f} TFLOP/s")
     if args.only in (None, "gather"):
         extra["gather_rmsnorm"] = bench_gather(torch, args)
         _log(f"gather: {json.dumps({k: round(v['us_per_call'], 3) for k, v in extra['gather_rmsnorm'].items()})} us")

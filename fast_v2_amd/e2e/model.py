@@ -36,6 +36,8 @@ class BlockDiffusionConfig:
     rope_theta: float = 1_000_000.0
     initializer_range: float = 0.02
     bd_size: int = 32
+    # the diffusion mask token (the last vocabulary id in the end-to-end workload)
+    mask_token_id: int = 152063
 
     @property
     def head_dim(self) -> int:
@@ -174,6 +176,13 @@ class BlockDiffusionLM(nn.Module):
                 mod.weight.normal_(0.0, std, generator=gen)
             elif isinstance(mod, RMSNorm):
                 mod.weight.fill_(1.0)
+        # A trained model never predicts its mask token. A random one can, and then the
+        # unmask rule writes the mask token back (generation_functions.py:789-799): the
+        # position stays masked and the block never completes. Its output row is zero, so
+        # its logit is 0 and never the argmax of ~N(0, 1) logits over the vocabulary.
+        mid = self.config.mask_token_id
+        if 0 <= mid < self.config.vocab_size:
+            self.lm_head.weight[mid].zero_()
 
     @torch.no_grad()
     def forward(self, input_ids: torch.Tensor, past_key_values, update_past_key_values: bool = False,

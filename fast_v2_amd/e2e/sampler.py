@@ -140,7 +140,7 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
              small_block_size: int = 8, mask_id: int = 152063, threshold: float = 0.9,
              use_block_cache: bool = True, stop_token: Optional[int] = None, pad_token: int = 0,
              impl=None, max_seq_len: Optional[int] = None, sync_timing: bool = True, policy=None,
-             bridge_policy=None):
+             bridge_policy=None, progress=None):
     """Generate for a batch of equal-length prompts [B, P]; returns (tokens [B, P + N + 1], stats).
 
     Equal prompt lengths are the config of the end-to-end workload; the reference's
@@ -148,7 +148,8 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
     ``policy(step, tok, conf, masked) -> (tok, unmask)`` replaces the greedy threshold
     rule when given (``step`` counts sampling steps from 0); ``bridge_policy(i, tok) ->
     tok`` likewise replaces the argmax token that opens each block (i = 0 after the
-    prefill, then one per commit)."""
+    prefill, then one per commit). ``progress(stats)`` is called on the host after every
+    forward is issued (it must not synchronise the device if timing matters)."""
     n_bridge = [0]
 
     def bridge(tok):
@@ -182,6 +183,8 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
             prefill_len = min_len // block_size * block_size
             logits = model(x[:, :prefill_len], cache, update_past_key_values=True)
             stats.forwards += 1
+            if progress is not None:
+                progress(stats)
             if min_len % block_size == 0:
                 x = torch.cat([x, bridge(logits[:, -1:].argmax(dim=-1))], dim=1)
         num_blocks = max_new_tokens // block_size + P // block_size
@@ -207,7 +210,17 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
                 mask = x[:, blk] == mask_id
                 left = bool((mask[:, s0:s1] & ~finished[:, None]).any())
                 first_masked = bool(mask[:, s0].any())
+                sub_steps = 0
                 while left:
+                    # every step unmasks at least one position of each unfinished row unless
+                    # the sampled token is the mask token itself, so a sub-block needs at most
+                    # small_block_size steps; far more means the model keeps predicting the
+                    # mask token (the reference loop would not end either)
+                    sub_steps += 1
+                    if sub_steps > 8 * small_block_size:
+                        raise RuntimeError(
+                            f"block {block_idx}, sub-block {sb}: no progress after {sub_steps - 1} steps "
+                            f"(the model keeps predicting the mask token {mask_id})")
                     if use_block_cache and len(block_cache) > 0 and not first_masked:
                         def sub_fwd(ids, pos, s0=s0):
                             return model(ids, cache, use_block_cache=True, block_past_key_values=block_cache,
@@ -230,6 +243,8 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
                             raw = full_fwd(x[:, blk], cache_pos)
                         row_offset = s0
                     stats.forwards += 1
+                    if progress is not None:
+                        progress(stats)
                     if fused:
                         # logits shifted by one position (:774): position i reads raw row
                         # max(row_offset + i - 1, 0)
@@ -237,6 +252,12 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
                                                   row_offset=row_offset, shift=1, finished=finished,
                                                   stop_token=stop_token, scratch=scratch)
                         n_unmasked, n_left, n_first, n_finished = scratch.counts.tolist()
+                        if n_unmasked == 0 and n_finished < B:
+                            # the rule unmasks at least one position of every unfinished row
+                            # with a finite confidence: no progress means non-finite logits
+                            raise RuntimeError(
+                                f"sampling step {len(stats.step_tokens)} (block {block_idx}, sub-block {sb}) "
+                                f"unmasked nothing with {n_left} masked positions left: non-finite logits?")
                         stats.step_tokens.append(n_unmasked)
                         left, first_masked = n_left > 0, n_first > 0
                         if n_finished == B:
@@ -262,6 +283,8 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
             # ---- commit (generation_functions.py:685-696)
             logits = model(x[:, blk], cache, update_past_key_values=True)
             stats.forwards += 1
+            if progress is not None:
+                progress(stats)
             stats.commits += 1
             nxt = bridge(logits[:, -1:].argmax(dim=-1))
             nxt[finished] = pad_token
