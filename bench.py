@@ -380,6 +380,52 @@ def calibrate_copies(torch):
     return res
 
 
+def _cpu_median_us(fn, seconds: float, min_calls: int = 3):
+    fn()  # warm
+    times = []
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end or len(times) < min_calls:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times) * 1e6, len(times)
+
+
+def cpu_baseline_gather(torch, seconds: float):
+    """Reference CPU path for gather + RMSNorm: ref_gather_input_rmsnorm
+    (cuda_bench/test_correctness.py:33-50) on the full bf16 [4096 x 3584] / 1024-row call."""
+    from fast_v2_amd import workloads
+    from oracle import gather_rmsnorm as og
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    wl = workloads.gather_rmsnorm_rows(seed=0)
+    us, calls = _cpu_median_us(lambda: og.ref_gather_input_rmsnorm(wl.hidden, wl.indices, wl.weight, wl.eps), seconds)
+    return {"value": round(us, 1), "unit": "us/call", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"ref_gather_input_rmsnorm (cuda_bench/test_correctness.py:33-50 restated in "
+                       f"oracle/gather_rmsnorm.py), the whole call (gathered + normed outputs); median of "
+                       f"{calls} calls over ~{seconds:.0f} s")}
+
+
+def cpu_baseline_prefill(torch, seconds: float):
+    """Reference CPU path for block-causal prefill: SDPA with the block-causal bool mask
+    (modeling.py:145-150, :398-411) on sequence 0 of the 4; value = 4 x that time."""
+    from fast_v2_amd import workloads
+    from oracle import attention as oa
+
+    n = len(os.sched_getaffinity(0))
+    torch.set_num_threads(n)
+    wl = workloads.block_prefill(seed=0)
+    q, k, v = wl.q[:1], wl.k[:1], wl.v[:1]
+    us, calls = _cpu_median_us(lambda: oa.sdpa_block_causal(q, k, v, wl.block, scaling=wl.scale), seconds,
+                               min_calls=2)
+    return {"value": round(4 * us, 1), "unit": "us/call", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": (f"SDPA with the block-causal mask (oracle/attention.py sdpa_block_causal), bf16, "
+                       f"sequence 0 of the 4 ([1, 4096, 28, 128] against 4 KV heads): median {us:.0f} us "
+                       f"over {calls} calls in ~{seconds:.0f} s; value = 4 x the sample (the sequences "
+                       f"are the same size)")}
+
+
 # ---------------------------------------------------------------------------
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -460,6 +506,12 @@ def main() -> int:
     if decode is not None and not args.no_cpu_baseline:
         _log("cpu baseline ...")
         cpu = cpu_baseline_decode(torch, wl, args.cpu_seconds)
+    if not args.no_cpu_baseline:
+        if "gather_rmsnorm" in extra:
+            extra["gather_rmsnorm"]["cpu_baseline"] = cpu_baseline_gather(torch, min(args.cpu_seconds, 5.0))
+        if "prefill" in extra:
+            _log("cpu baseline (prefill sample) ...")
+            extra["prefill"]["cpu_baseline"] = cpu_baseline_prefill(torch, args.cpu_seconds)
 
     if decode is not None:
         us = decode["us_per_step"]
