@@ -160,31 +160,23 @@ template <typename T, int WK, bool CAST, int VPL>
 __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArgs a) {
   constexpr int N = Vec16<T>::N;
   const int lane = threadIdx.x & (kWave - 1);
-  const int row = static_cast<int>(blockIdx.x) * 4 + (threadIdx.x >> 6);  // B * T < 2^31 (host check)
-  if (row >= a.B * a.T) return;
-  const int b = row / a.T;
-  const int t = row - b * a.T;
+  // grid (ceil(T / 4), B): four rows of one sequence per workgroup, no division
+  const int b = blockIdx.y;
+  const int t = static_cast<int>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (t >= a.T) return;
   const int nvec = a.H / N;
-  const int64_t src = a.idx[b * a.is_b + t];
+  // every address but the source row's is formed before the index arrives
+  const int64_t row = static_cast<int64_t>(b) * a.T + t;
+  const T* hbase = static_cast<const T*>(a.hidden) + b * a.hs_b;
+  u32x4* nrow = reinterpret_cast<u32x4*>(static_cast<T*>(a.normed) + row * a.H);
+  u32x4* grow = a.gathered ? reinterpret_cast<u32x4*>(static_cast<T*>(a.gathered) + row * a.H) : nullptr;
+  const int64_t src_raw = a.idx[b * a.is_b + t];
+  // an index outside [0, S) gives zero rows: the load reads row 0 and the values are
+  // replaced by zeros (a wave-uniform branch after the loads)
+  const bool valid = src_raw >= 0 && src_raw < a.S;
+  const int64_t src = valid ? src_raw : 0;
 
-  u32x4* nrow = reinterpret_cast<u32x4*>(static_cast<T*>(a.normed) + static_cast<int64_t>(row) * a.H);
-  u32x4* grow = a.gathered ? reinterpret_cast<u32x4*>(static_cast<T*>(a.gathered) + static_cast<int64_t>(row) * a.H)
-                           : nullptr;
-
-  if (src < 0 || src >= a.S) {
-    const u32x4 z = {0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int v = 0; v < VPL; ++v) {
-      const int c = lane + kWave * v;
-      if (c < nvec) {
-        __builtin_nontemporal_store(z, nrow + c);
-        if (grow) __builtin_nontemporal_store(z, grow + c);
-      }
-    }
-    return;
-  }
-
-  const u32x4* hrow = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.hidden) + b * a.hs_b + src * a.hs_s);
+  const u32x4* hrow = reinterpret_cast<const u32x4*>(hbase + src * a.hs_s);
   // All loads are issued unconditionally and back to back, so the whole row is in flight
   // at once. nvec lies in (64 (VPL - 1), 64 VPL], so only the last vector can run past the
   // row end: its index is clamped and its lanes past the end are zeroed afterwards.
@@ -199,6 +191,10 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
   for (int v = 0; v < VPL - 1; ++v) load_weight<T, WK, N>(a.weight, (lane + kWave * v) * N, w[v]);
   load_weight<T, WK, N>(a.weight, (last_in ? clast : nvec - 1) * N, w[VPL - 1]);
   if (!last_in) x[VPL - 1] = u32x4{0u, 0u, 0u, 0u};
+  if (!valid) {
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) x[v] = u32x4{0u, 0u, 0u, 0u};
+  }
 
   float ss = 0.f;
 #pragma unroll
@@ -209,7 +205,7 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
     for (int i = 0; i < N; ++i) ss += f[i] * f[i];
   }
   ss = wave_allreduce_sum(ss);
-  const float inv = 1.0f / sqrtf(ss / static_cast<float>(a.H) + a.eps);
+  const float inv = valid ? 1.0f / sqrtf(ss / static_cast<float>(a.H) + a.eps) : 0.f;
 
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
@@ -365,16 +361,17 @@ template <typename T>
 int launch_gather(const GatherArgs& a, bool vec, hipStream_t stream) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.T;
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
-  if (vec) {
+  if (vec && a.B <= 65535) {
+    const dim3 vgrid(static_cast<unsigned>((a.T + 3) / 4), static_cast<unsigned>(a.B));
     bool done;
     if (a.mode == FDLLM_NORM_PLAIN) {
-      done = launch_gather_vec<T, kWNone, false>(a, grid, stream);
+      done = launch_gather_vec<T, kWNone, false>(a, vgrid, stream);
     } else if (a.wdtype == FDLLM_DTYPE_F32) {
-      done = launch_gather_vec_mode<T, kW32>(a, grid, stream);
+      done = launch_gather_vec_mode<T, kW32>(a, vgrid, stream);
     } else if constexpr (!std::is_same<T, float>::value) {
       // 16-bit weights in the rows' own format; other combinations take the generic path
       const bool same = (a.wdtype == FDLLM_DTYPE_BF16) == std::is_same<T, bf16_t>::value;
-      done = same && launch_gather_vec_mode<T, kW16>(a, grid, stream);
+      done = same && launch_gather_vec_mode<T, kW16>(a, vgrid, stream);
     } else {
       done = false;
     }
