@@ -156,7 +156,7 @@ struct GatherArgs {
 // VPL = 16-byte vectors per lane (the whole row stays in registers). The norm form is a
 // template parameter, so the per-element code is straight-line. Outputs are written once
 // and not read again by this kernel: non-temporal (streaming) stores.
-template <typename T, int WK, bool CAST, int VPL>
+template <typename T, int WK, bool CAST, bool GATHERED, int VPL>
 __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArgs a) {
   constexpr int N = Vec16<T>::N;
   const int lane = threadIdx.x & (kWave - 1);
@@ -169,12 +169,21 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
   const int64_t row = static_cast<int64_t>(b) * a.T + t;
   const T* hbase = static_cast<const T*>(a.hidden) + b * a.hs_b;
   u32x4* nrow = reinterpret_cast<u32x4*>(static_cast<T*>(a.normed) + row * a.H);
-  u32x4* grow = a.gathered ? reinterpret_cast<u32x4*>(static_cast<T*>(a.gathered) + row * a.H) : nullptr;
-  const int64_t src_raw = a.idx[b * a.is_b + t];
-  // an index outside [0, S) gives zero rows: the load reads row 0 and the values are
-  // replaced by zeros (a wave-uniform branch after the loads)
-  const bool valid = src_raw >= 0 && src_raw < a.S;
-  const int64_t src = valid ? src_raw : 0;
+  u32x4* grow = GATHERED ? reinterpret_cast<u32x4*>(static_cast<T*>(a.gathered) + row * a.H) : nullptr;
+  const int64_t src = a.idx[b * a.is_b + t];
+  // an index outside [0, S) gives zero rows (a wave-uniform exit before any row load)
+  if (static_cast<uint64_t>(src) >= static_cast<uint64_t>(a.S)) {
+    const u32x4 z = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int c = lane + kWave * v;
+      if (c < nvec) {
+        __builtin_nontemporal_store(z, nrow + c);
+        if constexpr (GATHERED) __builtin_nontemporal_store(z, grow + c);
+      }
+    }
+    return;
+  }
 
   const u32x4* hrow = reinterpret_cast<const u32x4*>(hbase + src * a.hs_s);
   // All loads are issued unconditionally and back to back, so the whole row is in flight
@@ -191,10 +200,6 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
   for (int v = 0; v < VPL - 1; ++v) load_weight<T, WK, N>(a.weight, (lane + kWave * v) * N, w[v]);
   load_weight<T, WK, N>(a.weight, (last_in ? clast : nvec - 1) * N, w[VPL - 1]);
   if (!last_in) x[VPL - 1] = u32x4{0u, 0u, 0u, 0u};
-  if (!valid) {
-#pragma unroll
-    for (int v = 0; v < VPL; ++v) x[v] = u32x4{0u, 0u, 0u, 0u};
-  }
 
   float ss = 0.f;
 #pragma unroll
@@ -205,7 +210,7 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
     for (int i = 0; i < N; ++i) ss += f[i] * f[i];
   }
   ss = wave_allreduce_sum(ss);
-  const float inv = valid ? 1.0f / sqrtf(ss / static_cast<float>(a.H) + a.eps) : 0.f;
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(a.H) + a.eps);
 
 #pragma unroll
   for (int v = 0; v < VPL; ++v) {
@@ -216,7 +221,7 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
     const u32x4 o = Vec16<T>::pack(f);
     if (v < VPL - 1 || last_in) {
       const int c = lane + kWave * v;
-      if (grow) __builtin_nontemporal_store(x[v], grow + c);
+      if constexpr (GATHERED) __builtin_nontemporal_store(x[v], grow + c);
       __builtin_nontemporal_store(o, nrow + c);
     }
   }
@@ -324,14 +329,14 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(const ScatterArgs a) 
   }
 }
 
-template <typename T, int WK, bool CAST>
+template <typename T, int WK, bool CAST, bool GATHERED>
 bool launch_gather_vec(const GatherArgs& a, dim3 grid, hipStream_t stream) {
   const int nvec = a.H / Vec16<T>::N;
   const int vpl = (nvec + kWave - 1) / kWave;
   switch (vpl) {
-#define FDLLM_VPL_CASE(n)                                                        \
-  case n:                                                                        \
-    gather_rmsnorm_vec_kernel<T, WK, CAST, n><<<grid, dim3(256), 0, stream>>>(a); \
+#define FDLLM_VPL_CASE(n)                                                                  \
+  case n:                                                                                  \
+    gather_rmsnorm_vec_kernel<T, WK, CAST, GATHERED, n><<<grid, dim3(256), 0, stream>>>(a); \
     return true;
     FDLLM_VPL_CASE(1)
     FDLLM_VPL_CASE(2)
@@ -351,10 +356,16 @@ bool launch_gather_vec(const GatherArgs& a, dim3 grid, hipStream_t stream) {
   }
 }
 
+template <typename T, int WK, bool CAST>
+bool launch_gather_vec_out(const GatherArgs& a, dim3 grid, hipStream_t stream) {
+  return a.gathered ? launch_gather_vec<T, WK, CAST, true>(a, grid, stream)
+                    : launch_gather_vec<T, WK, CAST, false>(a, grid, stream);
+}
+
 template <typename T, int WK>
 bool launch_gather_vec_mode(const GatherArgs& a, dim3 grid, hipStream_t stream) {
-  return a.mode == FDLLM_NORM_WEIGHT_AFTER_CAST ? launch_gather_vec<T, WK, true>(a, grid, stream)
-                                                : launch_gather_vec<T, WK, false>(a, grid, stream);
+  return a.mode == FDLLM_NORM_WEIGHT_AFTER_CAST ? launch_gather_vec_out<T, WK, true>(a, grid, stream)
+                                                : launch_gather_vec_out<T, WK, false>(a, grid, stream);
 }
 
 template <typename T>
@@ -365,7 +376,7 @@ int launch_gather(const GatherArgs& a, bool vec, hipStream_t stream) {
     const dim3 vgrid(static_cast<unsigned>((a.T + 3) / 4), static_cast<unsigned>(a.B));
     bool done;
     if (a.mode == FDLLM_NORM_PLAIN) {
-      done = launch_gather_vec<T, kWNone, false>(a, vgrid, stream);
+      done = launch_gather_vec_out<T, kWNone, false>(a, vgrid, stream);
     } else if (a.wdtype == FDLLM_DTYPE_F32) {
       done = launch_gather_vec_mode<T, kW32>(a, vgrid, stream);
     } else if constexpr (!std::is_same<T, float>::value) {
