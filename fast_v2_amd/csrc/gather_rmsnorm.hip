@@ -160,9 +160,10 @@ template <typename T, int WK, bool CAST, bool GATHERED, int VPL>
 __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArgs a) {
   constexpr int N = Vec16<T>::N;
   const int lane = threadIdx.x & (kWave - 1);
-  // grid (ceil(T / 4), B): four rows of one sequence per workgroup, no division
+  // grid (ceil(T / 4), B): four rows of one sequence per workgroup, no division; the row
+  // is wave-uniform, so its index, bounds check and addresses live in scalar registers
   const int b = blockIdx.y;
-  const int t = static_cast<int>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int t = static_cast<int>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (t >= a.T) return;
   const int nvec = a.H / N;
   // every address but the source row's is formed before the index arrives
@@ -170,9 +171,13 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
   const T* hbase = static_cast<const T*>(a.hidden) + b * a.hs_b;
   u32x4* nrow = reinterpret_cast<u32x4*>(static_cast<T*>(a.normed) + row * a.H);
   u32x4* grow = GATHERED ? reinterpret_cast<u32x4*>(static_cast<T*>(a.gathered) + row * a.H) : nullptr;
+  const int64_t hs_s = a.hs_s;
+  // keep the row base and stride in registers ahead of the index load, so the row
+  // address is one multiply-add once the index arrives
+  __asm__ volatile("" : : "s"(hbase), "s"(hs_s));
   const int64_t src = a.idx[b * a.is_b + t];
   // an index outside [0, S) gives zero rows (a wave-uniform exit before any row load)
-  if (static_cast<uint64_t>(src) >= static_cast<uint64_t>(a.S)) {
+  if (__builtin_expect(static_cast<uint64_t>(src) >= static_cast<uint64_t>(a.S), 0)) {
     const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
@@ -185,7 +190,7 @@ __global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArg
     return;
   }
 
-  const u32x4* hrow = reinterpret_cast<const u32x4*>(hbase + src * a.hs_s);
+  const u32x4* hrow = reinterpret_cast<const u32x4*>(hbase + src * hs_s);
   // All loads are issued unconditionally and back to back, so the whole row is in flight
   // at once. nvec lies in (64 (VPL - 1), 64 VPL], so only the last vector can run past the
   // row end: its index is clamped and its lanes past the end are zeroed afterwards.
