@@ -1310,10 +1310,15 @@ template <bool F16, bool PAGED, bool SPLIT>
 __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) {
   constexpr int D = 128;
   constexpr int KT = 64;
-  constexpr int KS = D + 8;   // K row stride in LDS: 16-byte pad
-  constexpr int VS = D + 16;  // V row stride in LDS: 32-byte pad for the transposing reads
+  constexpr int KS = D + 8;  // K row stride in LDS: 16-byte pad
+  // V in two regions, columns 32 d + [0, 16) in the first and 32 d + [16, 32) in the
+  // second (row stride 80 elements each), the second shifted by 128 bytes past the
+  // first: the transposing reads of lanes 16-31 (the upper 16 columns of the rows lanes
+  // 0-15 read) then fall on the other half of the banks
+  constexpr int VS2 = 80;
+  constexpr int VOFF = KT * VS2 + 64;
   constexpr int KBUF = KT * KS;
-  constexpr int VBUF = KT * VS;
+  constexpr int VBUF = 2 * VOFF;
   __shared__ __attribute__((aligned(16))) uint16_t sKV[2][KBUF + VBUF];
 
   const int tid = threadIdx.x;
@@ -1455,7 +1460,8 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
     for (int i = 0; i < 2; ++i) {
       const int c = tid + 512 * i;
       *reinterpret_cast<u32x4*>(&sk[(c >> 4) * KS + (c & 15) * 8]) = sg.k[i];
-      *reinterpret_cast<u32x4*>(&sv[(c >> 4) * VS + (c & 15) * 8]) = sg.v[i];
+      *reinterpret_cast<u32x4*>(&sv[((c >> 1) & 1) * VOFF + (c >> 4) * VS2 + ((c >> 2) & 3) * 16 + (c & 1) * 8]) =
+          sg.v[i];
     }
   };
   auto compute_tile = [&](int buf, int kb) {
@@ -1530,9 +1536,10 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
       const int vr = 16 * kk + 4 * (g16 >> 1) + (l16 >> 2);
 #pragma unroll
       for (int dt = 0; dt < 4; ++dt) {
-        const int vc = 32 * dt + 16 * (g16 & 1) + 4 * (l16 & 3);
-        const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(&sv[vr * VS + vc]));
-        const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(&sv[(vr + 8) * VS + vc]));
+        // column 32 dt + 16 (g16 & 1) + 4 (l16 & 3) in the split layout
+        const int vi = (g16 & 1) * VOFF + 16 * dt + 4 * (l16 & 3);
+        const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(&sv[vi + vr * VS2]));
+        const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(&sv[vi + (vr + 8) * VS2]));
         acc[dt] = mfma32x32x16<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf, acc[dt]);
       }
     }
