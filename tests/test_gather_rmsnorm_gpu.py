@@ -131,6 +131,36 @@ def test_hidden_sizes_and_fp16(gpu, H, dtype):
     np.testing.assert_allclose(normed.float().cpu().numpy(), exp_n, atol=ATOL, rtol=RTOL)
 
 
+@pytest.mark.parametrize("H,dtype,tag", [
+    (2056, torch.bfloat16, "bf16"),   # 257 16-byte vectors: 5 per lane, the last one ragged
+    (6152, torch.bfloat16, "bf16"),   # 769 vectors: 13 per lane, the generic path
+    (8192, torch.float16, "f16"),     # 1024 vectors: the widest row held in registers
+    (3588, torch.float32, "f32"),     # fp32 rows, 897 vectors: the generic path
+])
+@pytest.mark.parametrize("mode", [og.NORM_WEIGHT_AFTER_CAST, og.NORM_PLAIN])
+def test_long_rows_with_bad_indices(gpu, H, dtype, tag, mode):
+    """Rows of 2 K - 8 K elements on the register and generic paths, with out-of-range
+    indices mixed in (zero rows, no read)."""
+    print(f"case long rows H={H} {tag} mode={mode}", flush=True)
+    g = torch.Generator().manual_seed(H + mode)
+    B, S, T = 3, 21, 11
+    hidden = (2 * torch.randn(B, S, H, generator=g)).to(dtype)
+    idx = torch.randint(0, S, (B, T), generator=g)
+    idx[0, 0] = -1
+    idx[1, T - 1] = S
+    idx[2, 5] = -(1 << 40)
+    w = (1 + 0.1 * torch.randn(H, generator=g)).to(dtype)
+    normed, gathered = ops.gather_rmsnorm(hidden.to(gpu), idx.to(gpu), w.to(gpu), 1e-6, mode, True)
+    normed, gathered = normed.float().cpu(), gathered.cpu()
+    ok = (idx >= 0) & (idx < S)
+    assert torch.count_nonzero(normed[~ok]) == 0 and torch.count_nonzero(gathered[~ok]) == 0
+    safe = idx.clamp(0, S - 1)
+    exp_g, exp_n = og.gather_rmsnorm_np(hidden.float().numpy(), safe.numpy(), w.float().numpy(), 1e-6, mode, tag)
+    okn = ok.numpy()
+    assert np.array_equal(gathered.float().numpy()[okn], exp_g[okn])
+    np.testing.assert_allclose(normed.numpy()[okn], exp_n[okn], atol=ATOL, rtol=RTOL)
+
+
 def test_strided_hidden_and_bad_indices(gpu):
     g = torch.Generator().manual_seed(3)
     base = torch.randn(2, 50, 2 * 512, generator=g).to(torch.bfloat16)
