@@ -164,8 +164,8 @@ def bench_decode(torch, args):
 def bench_decode_full(torch, args):
     """The same 16 sequences with all 32 block queries active (the full-block forward of a
     diffusion step): 224 query rows per KV head, run on the prefill kernel's 32x32 MFMA
-    tiles with key splits and the in-kernel merge. Same KV pools and page table layout as
-    the headline step, N(0, 1) on the device."""
+    tiles with key splits, then the merge kernel (two kernels per step). Same KV pools and
+    page table layout as the headline step, N(0, 1) on the device."""
     from fast_v2_amd import ops, workloads
 
     dev = torch.device("cuda", 0)

@@ -80,6 +80,7 @@ struct AttnParams {
   float* ws_o;       // [units, n_splits, rows_per_wg, D]
   float2* ws_ml;     // [units, n_splits, rows_per_wg]
   int* ws_cnt;       // [units] arrival counters of the split decode kernel (zero between calls)
+  int2* ws_unit;     // [units] (first slot, splits) written by the split prefill kernel for its merge
 };
 
 template <bool F16>
@@ -858,14 +859,15 @@ __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
 // 64-row worst case takes one pass of 512 threads; the splits are folded in
 // groups of eight whose loads are all issued before any is used (one memory
 // round trip up to eight splits), with the running maximum moved between groups.
-template <bool F16, int RS = 64>  // RS: partial rows per slot
+template <bool F16, int RS = 64, int AUX = kSc1>  // RS: partial rows per slot; AUX: load cache policy
 __device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh, int64_t slot0, int n_act, int tid,
-                                             int nthreads) {
+                                             int nthreads, int item_end = -1) {
   constexpr int D = 128;
   constexpr int GS = 8;
+  const int iend = item_end < 0 ? p.R * 8 : item_end;
   const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot0 * RS * D, 0, n_act * RS * D * 4, kBufferFlags);
   const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot0 * RS, 0, n_act * RS * 8, kBufferFlags);
-  for (int item = tid; item < p.R * 8; item += nthreads) {
+  for (int item = tid; item < iend; item += nthreads) {
     // columns 4 c8 + 32 j + (0..3), j = 0..3: the eight threads of a row read 128
     // contiguous bytes per load
     const int r = item >> 3;
@@ -881,11 +883,11 @@ __device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh
       for (int u = 0; u < GS; ++u) {
         // splits past n_act read as zero (outside the descriptor) and weigh nothing
         const int row = (s0 + u) * RS + r;
-        ml[u] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(mrsrc, row * 8, 0, kSc1));
+        ml[u] = __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(mrsrc, row * 8, 0, AUX));
 #pragma unroll
         for (int j = 0; j < 4; ++j)
           x[u][j] = __builtin_bit_cast(
-              f32x4, __builtin_amdgcn_raw_buffer_load_b128(orsrc, (row * D + c8 + 32 * j) * 4, 0, kSc1));
+              f32x4, __builtin_amdgcn_raw_buffer_load_b128(orsrc, (row * D + c8 + 32 * j) * 4, 0, AUX));
       }
       float mg = m;
 #pragma unroll
@@ -1566,9 +1568,14 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
 
   // ---- epilogue: rows of both lane halves are whole after the exchange of l
   l_run = halves_sum(l_run);
+  if constexpr (SPLIT) {
+    // the unit's (first slot, splits) for the merge kernel, rewritten on every call by
+    // the workgroup of split 0 (every unit has one)
+    if (split == 0 && tid == 0 && p.ws_unit != nullptr) p.ws_unit[b * p.Hkv + kvh] = make_int2(first, n_act);
+  }
   if (SPLIT && n_act > 1) {
-    // partial (O, m, l) of this key range: slot rows = the workgroup's 256 rows
-    const int unit = b * p.Hkv + kvh;
+    // partial (O, m, l) of this key range: slot rows = the workgroup's 256 rows; the
+    // merge kernel that follows on the stream folds them
     const int64_t slot0 = first;
     if (r < p.R) {
       const int64_t slot = slot0 + split;
@@ -1579,23 +1586,13 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
         for (int i = 0; i < 4; ++i)
           __builtin_amdgcn_raw_buffer_store_b128(
               __builtin_bit_cast(u32x4, f32x4{acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]}),
-              orsrc, (r * D + 32 * dt + 8 * i + 4 * h) * 4, 0, kSc1);
+              orsrc, (r * D + 32 * dt + 8 * i + 4 * h) * 4, 0, 0);
       if (h == 0) {
         const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot * 256, 0, 256 * 8, kBufferFlags);
         __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)), mrsrc, r * 8, 0,
-                                              kSc1);
+                                              0);
       }
     }
-    // last workgroup of the unit merges (the protocol of kv_split_decode_kernel)
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    __shared__ int s_last;
-    if (tid == 0)
-      s_last = __hip_atomic_fetch_add(&p.ws_cnt[unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_act - 1;
-    __syncthreads();
-    if (!s_last) return;
-    merge_splits<F16, 256>(p, b, kvh, slot0, n_act, tid, 512);
-    if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     return;
   }
   if (r < p.R) {
@@ -1611,6 +1608,24 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
                   pack2<F16>(acc[dt][e + 2] * inv, acc[dt][e + 3] * inv)};
       }
   }
+}
+
+// Merge of the split prefill kernel's partials: grid (row chunks of 32, units),
+// 256 threads = 32 rows x 8 column groups. The unit's slots and split count come from
+// the table the kernel wrote in the same call; units with one split were written by
+// the kernel itself. Spreading the merge over the whole chip instead of the last
+// workgroup of each unit matters here: a unit's partials are 224 rows x 520 bytes
+// per split, several hundred KB, more than one compute unit reads quickly.
+template <bool F16>
+__global__ __launch_bounds__(256) void kv_split_prefill_merge_kernel(const AttnParams p) {
+  const int unit = blockIdx.y;
+  const int2 e = p.ws_unit[unit];
+  if (e.y <= 1) return;
+  const int b = unit / p.Hkv;
+  const int kvh = unit - b * p.Hkv;
+  const int item0 = static_cast<int>(blockIdx.x) * 256;
+  merge_splits<F16, 256, 0>(p, b, kvh, e.x, e.y, item0 + static_cast<int>(threadIdx.x), 256,
+                            min(p.R * 8, item0 + 256));
 }
 
 // Merge the split partials of every (sequence, KV head, row block) with more than
@@ -1737,6 +1752,7 @@ struct Plan {
   bool decode;  // all-heads decode kernel (kv_decode_kernel)
   int MT, rows_per_wg, n_rb, n_splits, chunk, R;
   size_t ws_o_bytes, ws_ml_bytes;
+  size_t ws_unit_off;  // split prefill: byte offset of the unit table in the (m, l) region
 };
 
 // Split-KV decode plan. By default the kernel partitions the keys itself from the
@@ -1749,6 +1765,7 @@ constexpr size_t kCounterBytes = 64 * 1024;           // arrival counters at the
 
 int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
   FDLLM_CHECK_ARG(d != nullptr, "fdllm_kv_attn: null descriptor");
+  pl->ws_unit_off = 0;
   FDLLM_CHECK_ARG(d->dtype == FDLLM_DTYPE_BF16 || d->dtype == FDLLM_DTYPE_F16,
                   "fdllm_kv_attn: dtype %d unsupported (bf16 or fp16 only)", d->dtype);
   FDLLM_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128, "fdllm_kv_attn: head_dim %d unsupported (64 or 128)",
@@ -1893,7 +1910,8 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
       FDLLM_CHECK_ARG(slots * hkv < (int64_t{1} << 31) / 256, "fdllm_kv_attn: too many split slots");
       if (split_possible) {
         pl->ws_o_bytes = static_cast<size_t>(slots) * hkv * 256 * d->head_dim * sizeof(float);
-        pl->ws_ml_bytes = static_cast<size_t>(slots) * hkv * 256 * sizeof(float2);
+        pl->ws_unit_off = static_cast<size_t>(slots) * hkv * 256 * sizeof(float2);
+        pl->ws_ml_bytes = pl->ws_unit_off + static_cast<size_t>(B) * hkv * sizeof(int2);
       } else {
         pl->ws_o_bytes = pl->ws_ml_bytes = 0;
       }
@@ -2007,9 +2025,11 @@ void launch_attn(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
 }
 
 // Workspace layout: a fixed 64 KiB of arrival counters (one int per (sequence,
-// KV head)), the (m, l) pairs of every split partial, then the partial rows. The
-// counter region has the same place and size for every call, so partials of one
-// call never land where a later call with more sequences keeps its counters.
+// KV head)), the (m, l) pairs of every split partial (for the split prefill kernel
+// followed by its table of (first slot, splits) per (sequence, KV head)), then the
+// partial rows. The counter region has the same place and size for every call, so
+// partials of one call never land where a later call with more sequences keeps its
+// counters.
 inline size_t counter_bytes(const fdllm_kv_attn_desc*) { return kCounterBytes; }
 
 inline size_t plan_workspace_bytes(const fdllm_kv_attn_desc* d, const Plan& pl) {
@@ -2098,10 +2118,12 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
     w += counter_bytes(d);
     p.ws_ml = reinterpret_cast<float2*>(w);
     p.ws_o = reinterpret_cast<float*>(w + align256(pl.ws_ml_bytes));
+    p.ws_unit = pl.kind == kPlanSplitPrefill ? reinterpret_cast<int2*>(w + pl.ws_unit_off) : nullptr;
   } else {
     p.ws_cnt = nullptr;
     p.ws_ml = nullptr;
     p.ws_o = nullptr;
+    p.ws_unit = nullptr;
   }
   const bool f16 = d->dtype == FDLLM_DTYPE_F16;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -2138,6 +2160,12 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
     } else {
       if (paged) kv_prefill_kernel<false, true, true><<<grid, dim3(512), 0, s>>>(p);
       else kv_prefill_kernel<false, false, true><<<grid, dim3(512), 0, s>>>(p);
+    }
+    if (p.ws_unit != nullptr) {
+      // units = B * Hkv; 32 rows per workgroup
+      const dim3 mgrid(static_cast<unsigned>((pl.R + 31) / 32), static_cast<unsigned>(d->batch * d->num_kv_heads));
+      if (f16) kv_split_prefill_merge_kernel<true><<<mgrid, dim3(256), 0, s>>>(p);
+      else kv_split_prefill_merge_kernel<false><<<mgrid, dim3(256), 0, s>>>(p);
     }
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }

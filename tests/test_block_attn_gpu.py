@@ -419,11 +419,55 @@ def test_prefill_kernel(gpu, case):
         _check(out, exp)
 
 
+def test_split_prefill_merge_under_graph_replay(gpu):
+    """Full-block calls (32 active queries): the split kernel writes each (sequence, KV
+    head)'s slots and split count on every call for the merge kernel. Eager calls of
+    two batch sizes in turn on one workspace (a different table at a different offset
+    each time) keep their results, and a captured call replayed several times, with
+    those eager calls in between, matches the eager result on every replay."""
+    wl = workloads.kv_decode_paged(seed=8, batch=16, active=32)
+    q, kp, vp = wl.q.to(gpu), wl.k_pool.to(gpu), wl.v_pool.to(gpu)
+    pt, sl = wl.page_table.to(gpu), wl.seqlens.to(gpu)
+    other = workloads.kv_decode_paged(seed=9, batch=5, active=32, min_prefix=200, max_prefix=3500)
+    oq, okp, ovp = other.q.to(gpu), other.k_pool.to(gpu), other.v_pool.to(gpu)
+    opt, osl = other.page_table.to(gpu), other.seqlens.to(gpu)
+    print("case full-block graph replay B=16 / eager B=5", flush=True)
+
+    def call():
+        return ops.block_attn(q, kp, vp, sl, wl.scale, page_table=pt, page_size=wl.page_size)
+
+    def other_call():
+        return ops.block_attn(oq, okp, ovp, osl, other.scale, page_table=opt, page_size=other.page_size)
+
+    eager = call()
+    _check(eager, oa.attention_np(wl.q.float(), wl.k_pool.float(), wl.v_pool.float(), wl.seqlens, wl.scale,
+                                  page_table=wl.page_table, page_size=wl.page_size))
+    other_eager = other_call()
+    _check(other_eager, oa.attention_np(other.q.float(), other.k_pool.float(), other.v_pool.float(), other.seqlens,
+                                        other.scale, page_table=other.page_table, page_size=other.page_size))
+    assert torch.equal(call(), eager)
+    s = torch.cuda.Stream(gpu)
+    s.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(s):
+        call()  # workspace for this stream exists before capture
+        torch.cuda.synchronize(gpu)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            out = call()
+    torch.cuda.current_stream(gpu).wait_stream(s)
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        assert torch.equal(out, eager)
+        assert torch.equal(other_call(), other_eager)
+        torch.cuda.synchronize(gpu)
+
+
 @pytest.mark.parametrize("case", ["bs16_paged32", "ragged_contig", "fp16_paged64", "fixed_chunks", "gqa8_256_rows"])
 def test_block_decode_split_prefill_kernel(gpu, case):
     """A whole 32-token block per step (64 < rows per KV head <= 256): the prefill
-    kernel's math with split keys and the in-kernel merge, against the oracle and
-    against the general kernel on the same call."""
+    kernel's math with split keys and the merge kernel that follows it, against the
+    oracle and against the general kernel on the same call."""
     split, dtype, decode_args = 0, torch.bfloat16, {}
     if case == "bs16_paged32":
         wl = workloads.kv_decode_paged(seed=0, active=32)
