@@ -168,10 +168,11 @@ typedef struct fdllm_kv_attn_desc {
 /* Bytes of device workspace fdllm_kv_attn_fwd needs for `desc` (0 when the call
  * is not split over several workgroups per KV head). The workspace starts with
  * 64 KiB of arrival counters (one int per (sequence, KV head)), followed by the
- * per-split partial results (running max, sum and unnormalised output rows). For
- * sub-block decode shapes (at most 64 query rows per KV head) the last workgroup
- * of a (sequence, KV head) to finish merges them; for the others a second kernel
- * on the same stream does. The workspace must be zero-filled once when it is
+ * per-split partial results (running max, sum and unnormalised output rows). The
+ * split-KV decode kernel (the default for at most 64 query rows per KV head)
+ * merges them in the last workgroup of a (sequence, KV head) to finish; the other
+ * kernels leave them to a second kernel on the same stream. The workspace must be
+ * zero-filled once when it is
  * allocated: every call leaves the counters at zero again and writes every
  * partial it reads, so one workspace then serves any sequence of calls of any
  * sizes. Calls that may overlap in time (different streams) need separate
