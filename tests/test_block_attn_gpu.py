@@ -463,7 +463,8 @@ def test_split_prefill_merge_under_graph_replay(gpu):
         torch.cuda.synchronize(gpu)
 
 
-@pytest.mark.parametrize("case", ["bs16_paged32", "ragged_contig", "fp16_paged64", "fixed_chunks", "gqa8_256_rows"])
+@pytest.mark.parametrize("case", ["bs16_paged32", "ragged_contig", "fp16_paged64", "fixed_chunks", "gqa8_256_rows",
+                                  "rows91_contig"])
 def test_block_decode_split_prefill_kernel(gpu, case):
     """A whole 32-token block per step (64 < rows per KV head <= 256): the prefill
     kernel's math with split keys and the merge kernel that follows it, against the
@@ -489,6 +490,8 @@ def test_block_decode_split_prefill_kernel(gpu, case):
     else:
         g = torch.Generator().manual_seed(12)
         B, Sq, Hq, Hkv, D, S = 5, 32, 28, 4, 128, 3000
+        if case == "rows91_contig":  # 13 queries x GQA 7: the merge's last 32-row chunk holds 27 rows
+            Sq = 13
         q = torch.randn(B, Sq, Hq, D, generator=g).to(dtype)
         kc = torch.randn(B, S, Hkv, D, generator=g).to(dtype)
         vc = torch.randn(B, S, Hkv, D, generator=g).to(dtype)
