@@ -148,3 +148,25 @@ def test_workspace_size_for_the_decode_workload(lib):
     d.max_seqlen = 64
     assert lib.fdllm_kv_attn_workspace_size(ctypes.byref(d), ctypes.byref(size)) == 0
     assert size.value == 0
+
+
+def test_workspace_size_for_the_full_block_workload(lib):
+    """The bs16 full-block plan (32 queries x GQA 7 = 224 rows per KV head) splits each
+    KV head's keys over 64 slots of 256 rows, one workgroup per compute unit. Its
+    workspace holds the 64 KiB of counters, an fp32 (m, l) pair per slot row, one
+    (first slot, splits) pair per (sequence, KV head) for the merge kernel (padded to
+    256 bytes), and the fp32 partial rows."""
+    from fast_v2_amd import _ffi
+    d = _ffi.KVAttnDesc()
+    d.dtype = _ffi.DTYPE_BF16
+    B, Hkv, D = 16, 4, 128
+    d.batch, d.q_len, d.num_q_heads, d.num_kv_heads, d.head_dim = B, 32, 28, Hkv, D
+    d.k_stride_h = d.v_stride_h = D
+    d.max_seqlen = 4128
+    d.softmax_scale = D ** -0.5
+    size = ctypes.c_size_t(0)
+    assert lib.fdllm_kv_attn_workspace_size(ctypes.byref(d), ctypes.byref(size)) == 0
+    slot_rows = 64 * Hkv * 256
+    ml_and_table = slot_rows * 8 + B * Hkv * 8
+    ml_and_table = (ml_and_table + 255) // 256 * 256
+    assert size.value == 64 * 1024 + ml_and_table + slot_rows * D * 4
