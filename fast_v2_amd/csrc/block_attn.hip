@@ -854,16 +854,16 @@ __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
   return dp;
 }
 
-// Merge of the split partials of one (sequence, KV head) unit, run by the last
-// workgroup of the unit to finish. One work item per (row, 16 columns), so the
-// 64-row worst case takes one pass of 512 threads; the splits are folded in
-// groups of eight whose loads are all issued before any is used (one memory
-// round trip up to eight splits), with the running maximum moved between groups.
-template <bool F16, int RS = 64, int AUX = kSc1>  // RS: partial rows per slot; AUX: load cache policy
+// Merge of the split partials of one (sequence, KV head) unit. One work item per
+// (row, 16 columns), so the 64-row worst case takes one pass of 512 threads; the
+// splits are folded in groups of GS whose loads are all issued before any is used
+// (one memory round trip per group), with the running maximum moved between groups.
+// merge_splits_n picks GS = n_act up to eight: loads of splits past n_act would read
+// zero without memory traffic, but each still takes the texture unit's address cycles.
+template <bool F16, int RS = 64, int AUX = kSc1, int GS = 8>  // RS: partial rows per slot; AUX: load cache policy
 __device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh, int64_t slot0, int n_act, int tid,
                                              int nthreads, int item_end = -1) {
   constexpr int D = 128;
-  constexpr int GS = 8;
   const int iend = item_end < 0 ? p.R * 8 : item_end;
   const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot0 * RS * D, 0, n_act * RS * D * 4, kBufferFlags);
   const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot0 * RS, 0, n_act * RS * 8, kBufferFlags);
@@ -915,6 +915,20 @@ __device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh
     for (int j = 0; j < 4; ++j)
       *reinterpret_cast<u32x2*>(orow + 32 * j) =
           u32x2{pack2<F16>(o[j][0] * inv, o[j][1] * inv), pack2<F16>(o[j][2] * inv, o[j][3] * inv)};
+  }
+}
+
+template <bool F16, int RS = 64, int AUX = kSc1>
+__device__ __forceinline__ void merge_splits_n(const AttnParams& p, int b, int kvh, int64_t slot0, int n_act,
+                                               int tid, int nthreads, int item_end = -1) {
+  switch (n_act) {  // uniform over the workgroup
+    case 2: merge_splits<F16, RS, AUX, 2>(p, b, kvh, slot0, n_act, tid, nthreads, item_end); break;
+    case 3: merge_splits<F16, RS, AUX, 3>(p, b, kvh, slot0, n_act, tid, nthreads, item_end); break;
+    case 4: merge_splits<F16, RS, AUX, 4>(p, b, kvh, slot0, n_act, tid, nthreads, item_end); break;
+    case 5: merge_splits<F16, RS, AUX, 5>(p, b, kvh, slot0, n_act, tid, nthreads, item_end); break;
+    case 6: merge_splits<F16, RS, AUX, 6>(p, b, kvh, slot0, n_act, tid, nthreads, item_end); break;
+    case 7: merge_splits<F16, RS, AUX, 7>(p, b, kvh, slot0, n_act, tid, nthreads, item_end); break;
+    default: merge_splits<F16, RS, AUX, 8>(p, b, kvh, slot0, n_act, tid, nthreads, item_end); break;
   }
 }
 
@@ -1252,7 +1266,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
     s_last = __hip_atomic_fetch_add(&p.ws_cnt[unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_act - 1;
   __syncthreads();
   if (!s_last) return;
-  merge_splits<F16>(p, b, kvh, slot0, n_act, tid, 512);
+  merge_splits_n<F16>(p, b, kvh, slot0, n_act, tid, 512);
   if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
 }
 
@@ -1624,8 +1638,8 @@ __global__ __launch_bounds__(256) void kv_split_prefill_merge_kernel(const AttnP
   const int b = unit / p.Hkv;
   const int kvh = unit - b * p.Hkv;
   const int item0 = static_cast<int>(blockIdx.x) * 256;
-  merge_splits<F16, 256, 0>(p, b, kvh, e.x, e.y, item0 + static_cast<int>(threadIdx.x), 256,
-                            min(p.R * 8, item0 + 256));
+  merge_splits_n<F16, 256, 0>(p, b, kvh, e.x, e.y, item0 + static_cast<int>(threadIdx.x), 256,
+                              min(p.R * 8, item0 + 256));
 }
 
 // Merge the split partials of every (sequence, KV head, row block) with more than
