@@ -858,8 +858,9 @@ __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
 // (row, 16 columns), so the 64-row worst case takes one pass of 512 threads; the
 // splits are folded in groups of GS whose loads are all issued before any is used
 // (one memory round trip per group), with the running maximum moved between groups.
-// merge_splits_n picks GS = n_act up to eight: loads of splits past n_act would read
-// zero without memory traffic, but each still takes the texture unit's address cycles.
+// merge_splits_n picks GS = n_act up to eight (equal groups beyond): loads of splits past
+// n_act would read zero without memory traffic, but each still takes the texture unit's
+// address cycles.
 template <bool F16, int RS = 64, int AUX = kSc1, int GS = 8>  // RS: partial rows per slot; AUX: load cache policy
 __device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh, int64_t slot0, int n_act, int tid,
                                              int nthreads, int item_end = -1) {
@@ -921,7 +922,9 @@ __device__ __forceinline__ void merge_splits(const AttnParams& p, int b, int kvh
 template <bool F16, int RS = 64, int AUX = kSc1>
 __device__ __forceinline__ void merge_splits_n(const AttnParams& p, int b, int kvh, int64_t slot0, int n_act,
                                                int tid, int nthreads, int item_end = -1) {
-  switch (n_act) {  // uniform over the workgroup
+  // groups of equal size, at most eight: 9 splits take two groups of five, not 8 + 1
+  const int groups = (n_act + 7) >> 3;
+  switch ((n_act + groups - 1) / groups) {  // uniform over the workgroup
     case 2: merge_splits<F16, RS, AUX, 2>(p, b, kvh, slot0, n_act, tid, nthreads, item_end); break;
     case 3: merge_splits<F16, RS, AUX, 3>(p, b, kvh, slot0, n_act, tid, nthreads, item_end); break;
     case 4: merge_splits<F16, RS, AUX, 4>(p, b, kvh, slot0, n_act, tid, nthreads, item_end); break;
