@@ -15,14 +15,16 @@ Differences, by design:
     (fused_sparse_extension.py:81); here only the selected rows are read, once.
   * The model-path wrapper computes weight * normalized.to(dtype) inside the
     kernel (the Fast_dLLM_QwenRMSNorm order, modeling.py:427-432), one launch.
-  * A missing library raises RuntimeError instead of latching a silent None:
-    on a GPU the native path either runs or fails loudly. ``None`` is still
-    returned where the reference returns it for data reasons (hidden states
-    not on a GPU, a layernorm without a weight), so the caller's PyTorch path
-    (modeling.py:879-890) handles those exactly as before.
+  * Load failure keeps the reference's contract (fused_sparse_extension.py:17-48):
+    ``get_fused_ops()`` logs the reason once at ERROR level, latches the failure
+    and returns ``None`` on this and every later call, and
+    ``fused_gather_input_rmsnorm_pair`` then returns ``None`` so the caller takes
+    its PyTorch path (modeling.py:879-890). Nothing in this module computes on
+    the CPU; the ops of ``ops`` itself still raise without the library.
 """
 from __future__ import annotations
 
+import logging
 from typing import Optional, Tuple
 
 import torch
@@ -62,14 +64,26 @@ class _FusedOps:
         return [gathered, normed]
 
 
+_LOG = logging.getLogger(__name__)
 _OPS: Optional[_FusedOps] = None
+_OPS_FAILED = False
 
 
-def get_fused_ops() -> _FusedOps:
-    """Load libfdllm_hip.so once and return the op table; raises RuntimeError if unavailable."""
-    global _OPS
+def get_fused_ops() -> Optional[_FusedOps]:
+    """Load libfdllm_hip.so once and return the op table, or None if it cannot load.
+
+    The first failure is logged with its reason and latched: later calls return
+    None without trying again (fused_sparse_extension.py:25-48)."""
+    global _OPS, _OPS_FAILED
+    if _OPS_FAILED:
+        return None
     if _OPS is None:
-        _ffi.lib()
+        try:
+            _ffi.lib()
+        except Exception as exc:  # a missing or unloadable library: the caller falls back
+            _OPS_FAILED = True
+            _LOG.error("fused gather+RMSNorm ops unavailable, callers fall back to PyTorch: %s", exc)
+            return None
         _OPS = _FusedOps()
     return _OPS
 
@@ -83,17 +97,19 @@ def fused_gather_input_rmsnorm_pair(
 
     hidden_states (B, S, H); token_indices (B, T); input_layernorm has .weight and
     .variance_epsilon (default 1e-6). Returns (selected_hidden, selected_norm) in
-    hidden_states' dtype, or None when hidden_states is not on a GPU or the module
-    has no weight (the reference's contract, fused_sparse_extension.py:70-78).
+    hidden_states' dtype, or None when hidden_states is not on a GPU, the library
+    cannot load, or the module has no weight (the reference's contract,
+    fused_sparse_extension.py:70-78).
     """
     if not hidden_states.is_cuda:
+        return None
+    if get_fused_ops() is None:
         return None
     w = getattr(input_layernorm, "weight", None)
     if w is None:
         return None
     eps = getattr(input_layernorm, "variance_epsilon", 1e-6)
     eps = float(eps.item() if isinstance(eps, torch.Tensor) else eps)
-    get_fused_ops()
     dt = hidden_states.dtype
     if w.dtype == dt:
         normed, gathered = ops.gather_rmsnorm(hidden_states, token_indices, w.detach(), eps,

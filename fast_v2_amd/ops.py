@@ -54,16 +54,26 @@ class _Workspace:
     arrival counters must start at zero, and every call leaves them at zero.
     Partials are written before they are read, so nothing else needs clearing;
     calls on one stream run in order and may share the buffer.
+
+    A buffer that is outgrown is retired, never freed: a HIP graph captured
+    earlier on the stream keeps its address and writes counters and partials
+    there on every replay, so the memory must not return to the caching
+    allocator while the process may still replay such a graph. Each retired
+    buffer keeps its counters at zero (every call leaves them so), so a replay
+    after any number of larger calls still starts from a clean state.
     """
 
     def __init__(self) -> None:
         self._bufs: dict = {}
+        self._retired: list = []
 
     def get(self, nbytes: int, device: torch.device) -> torch.Tensor:
         stream = torch.cuda.current_stream(device)
         key = (device.index, stream.cuda_stream)
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
+            if buf is not None:
+                self._retired.append(buf)
             buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
             self._bufs[key] = buf
         return buf

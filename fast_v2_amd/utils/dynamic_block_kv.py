@@ -30,12 +30,15 @@ class DynamicBlockKV:
         self.batch_size = batch_size
 
     def write_full(self, layer_idx, k, v) -> None:
-        """Overwrite the whole block for a layer. k, v: [B, Hkv, block_size, D]."""
+        """Replace every row of ``layer_idx``'s block with ``k`` / ``v`` (both BHSD, all
+        ``block_size`` positions), as the dense seed step of a block does."""
         self.k[layer_idx].copy_(k)
         self.v[layer_idx].copy_(v)
 
     def write(self, layer_idx, k, v, token_indices) -> None:
-        """Scatter selected positions. k, v: [B, Hkv, n, D]; token_indices: [B, n]."""
+        """Store ``n`` recomputed rows per sequence: row ``i`` of ``k`` / ``v`` (BHSD, length
+        ``n``) lands at block position ``token_indices[b, i]``; positions not listed keep
+        their previous contents."""
         if k.dim() != 4 or k.shape != v.shape or token_indices.shape != (k.shape[0], k.shape[2]):
             raise RuntimeError("DynamicBlockKV.write: expected k, v [B, Hkv, n, D] and token_indices [B, n]")
         ops.kv_cache_write(k.transpose(1, 2), v.transpose(1, 2),
@@ -43,12 +46,14 @@ class DynamicBlockKV:
                            positions=token_indices)
 
     def get(self, layer_idx):
+        """The (k, v) buffers of ``layer_idx`` themselves, not copies."""
         return self.k[layer_idx], self.v[layer_idx]
 
     def reset(self) -> None:
-        """Nothing to clear: the dense seed step overwrites every position each block."""
+        """No-op: each block opens with a dense write that covers every position."""
 
     def compact_batch(self, active_indices) -> None:
+        """Keep only the sequences in ``active_indices`` (in that order)."""
         for L in self.k:
             self.k[L] = self.k[L][active_indices].contiguous()
             self.v[L] = self.v[L][active_indices].contiguous()

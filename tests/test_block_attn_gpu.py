@@ -281,6 +281,50 @@ def test_split_decode_counters_rearm_under_graph_replay(gpu):
         torch.cuda.synchronize(gpu)
 
 
+def test_workspace_growth_keeps_captured_graph_valid(gpu):
+    """A graph captured with a sub-block decode call keeps the stream's workspace
+    address; a later, larger full-block call on the same stream grows the workspace.
+    The old buffer must stay allocated (never handed back to the allocator), so every
+    replay after the growth is still bit-identical to the eager result."""
+    small = workloads.kv_decode_paged(seed=10, batch=4, min_prefix=1024, max_prefix=2048)
+    big = workloads.kv_decode_paged(seed=11, batch=16, active=32)
+    sq, skp, svp = small.q.to(gpu), small.k_pool.to(gpu), small.v_pool.to(gpu)
+    spt, ssl = small.page_table.to(gpu), small.seqlens.to(gpu)
+    bq, bkp, bvp = big.q.to(gpu), big.k_pool.to(gpu), big.v_pool.to(gpu)
+    bpt, bsl = big.page_table.to(gpu), big.seqlens.to(gpu)
+    print("case workspace growth: graph B=4 sub-block, eager B=16 full block", flush=True)
+
+    def small_call():
+        return ops.block_attn(sq, skp, svp, ssl, small.scale, page_table=spt, page_size=small.page_size)
+
+    def big_call():
+        return ops.block_attn(bq, bkp, bvp, bsl, big.scale, page_table=bpt, page_size=big.page_size)
+
+    s = torch.cuda.Stream(gpu)
+    s.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(s):
+        eager = small_call()  # creates this stream's (small) workspace
+        torch.cuda.synchronize(gpu)
+        ws_small = ops._WORKSPACE.get(0, gpu).data_ptr()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            out = small_call()
+        big_eager = big_call()  # grows the workspace of the same stream
+        torch.cuda.synchronize(gpu)
+        assert ops._WORKSPACE.get(0, gpu).data_ptr() != ws_small, "the full-block call did not grow the workspace"
+        # churn the caching allocator: a freed workspace would be handed out here
+        junk = [torch.full((1 << 20,), 7, dtype=torch.uint8, device=gpu) for _ in range(8)]
+        for _ in range(4):
+            graph.replay()
+            assert torch.equal(big_call(), big_eager)
+            torch.cuda.synchronize(gpu)
+            assert torch.equal(out, eager)
+        del junk
+    torch.cuda.current_stream(gpu).wait_stream(s)
+    _check(eager, oa.attention_np(small.q.float(), small.k_pool.float(), small.v_pool.float(), small.seqlens,
+                                  small.scale, page_table=small.page_table, page_size=small.page_size))
+
+
 def test_workspace_reuse_across_shapes(gpu):
     """One workspace serves consecutive split calls of different sizes: a large call
     after a small one must not merge partials the small call left behind."""

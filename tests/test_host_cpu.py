@@ -83,6 +83,60 @@ def test_fused_sparse_extension_returns_none_for_cpu_hidden():
     assert fse.fused_gather_input_rmsnorm_pair(h, torch.zeros(1, 2, dtype=torch.long), Norm()) is None
 
 
+_LATCH_PROBE = r"""
+import logging, sys
+import torch
+from fast_v2_amd.cuda_bench import fused_sparse_extension as fse
+
+records = []
+class H(logging.Handler):
+    def emit(self, r):
+        records.append(r)
+logging.getLogger(fse.__name__).addHandler(H())
+
+class FakeCudaHidden:          # only .is_cuda is read before the library check
+    is_cuda = True
+class Norm(torch.nn.Module):
+    def __init__(self):
+        super().__init__()
+        self.weight = torch.nn.Parameter(torch.ones(64))
+        self.variance_epsilon = 1e-6
+
+first = fse.get_fused_ops()
+second = fse.get_fused_ops()
+pair = fse.fused_gather_input_rmsnorm_pair(FakeCudaHidden(), torch.zeros(1, 2, dtype=torch.long), Norm())
+errors = [r for r in records if r.levelno >= logging.ERROR]
+print(first is None, second is None, pair is None, len(errors), fse._OPS_FAILED)
+"""
+
+
+def test_get_fused_ops_latches_a_load_failure(tmp_path):
+    """A library that cannot load: get_fused_ops() returns None, logs once and latches
+    (reference cuda_bench/fused_sparse_extension.py:25-48), and the model-path wrapper
+    returns None so the caller takes its PyTorch path (:70-78)."""
+    import os
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    env = dict(os.environ, FDLLM_HIP_LIB=str(tmp_path / "missing" / "libfdllm_hip.so"))
+    root = Path(__file__).resolve().parents[1]
+    proc = subprocess.run([sys.executable, "-c", _LATCH_PROBE], cwd=root, env=env, capture_output=True,
+                          text=True, timeout=300)
+    assert proc.returncode == 0, proc.stderr
+    assert proc.stdout.split() == ["True", "True", "True", "1", "True"], proc.stdout
+
+
+def test_get_fused_ops_loads_the_built_library():
+    if not _ffi.LIB_PATH.exists():
+        pytest.skip("libfdllm_hip.so not built")
+    ext = fse.get_fused_ops()
+    assert ext is not None and fse.get_fused_ops() is ext
+    for name in ("gather_rmsnorm_cuda", "scatter_and_return_cuda", "fused_select_norm",
+                 "fused_gather_input_rmsnorm_pair"):
+        assert callable(getattr(ext, name))
+
+
 def test_meta_implementations():
     q = torch.empty(2, 8, 28, 128, dtype=torch.bfloat16, device="meta")
     k = torch.empty(2, 512, 4, 128, dtype=torch.bfloat16, device="meta")
