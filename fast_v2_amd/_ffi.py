@@ -66,6 +66,8 @@ class KVAttnDesc(ctypes.Structure):
 ATTN_NO_DECODE_KERNEL = 1
 ATTN_ALL_HEADS_DECODE = 2
 
+KV_ATTN_SCRATCH_BYTES = 48 * 1024 * 1024  # FDLLM_KV_ATTN_SCRATCH_BYTES
+
 
 class RopeKVDesc(ctypes.Structure):
     """Mirror of ``fdllm_rope_kv_desc`` (include/fdllm_hip.h)."""
@@ -108,6 +110,7 @@ SIGNATURES = {
     ]),
     "fdllm_kv_attn_workspace_size": (_c_int, [ctypes.POINTER(KVAttnDesc), ctypes.POINTER(_c_sz)]),
     "fdllm_kv_attn_fwd": (_c_int, [ctypes.POINTER(KVAttnDesc), _c_vp, _c_sz, _c_vp]),
+    "fdllm_kv_attn_fwd_noalloc": (_c_int, [ctypes.POINTER(KVAttnDesc), _c_vp]),
     "fdllm_kv_cache_write": (_c_int, [
         _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,   # k_new, v_new, strides
         _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,   # k_cache, v_cache, strides

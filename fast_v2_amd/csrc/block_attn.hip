@@ -35,6 +35,7 @@
 //     splits' loads in flight). The kernel boundary orders the two, so no
 //     device-scope fence or counter is needed.
 #include <algorithm>
+#include <mutex>
 
 #include "fdllm_common.h"
 
@@ -2066,12 +2067,18 @@ extern "C" int fdllm_kv_attn_workspace_size(const fdllm_kv_attn_desc* desc, size
   return FDLLM_OK;
 }
 
-extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
-  using namespace fdllm;
-  Plan pl;
-  const int rc = make_plan(d, &pl);
-  if (rc != FDLLM_OK) return rc;
+// The library's attention scratch (one copy per device; see fdllm_kv_attn_fwd_noalloc).
+// In host code `scratch` names a host-side stand-in: kernels receive the device
+// address that hipGetSymbolAddress returns for it, never the name itself.
+static __device__ __align__(256) unsigned char scratch[FDLLM_KV_ATTN_SCRATCH_BYTES];
+
+namespace fdllm {
+namespace {
+
+// Validates `d` against its plan and launches the kernels on `stream`, with the
+// caller's workspace or the library's scratch (see fdllm_kv_attn_fwd_noalloc).
+int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace, size_t workspace_bytes,
+                   void* stream) {
   if (d->batch == 0 || d->q_len == 0) return FDLLM_OK;
   FDLLM_CHECK_ARG(d->q && d->k && d->v && d->out && d->seqlens, "fdllm_kv_attn_fwd: null pointer");
   FDLLM_CHECK_ARG(aligned16(d->q) && aligned16(d->k) && aligned16(d->v) && aligned16(d->out),
@@ -2206,6 +2213,105 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
     else launch_attn<64, 4>(p, f16, grid, s);
   }
   FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
+}
+
+// ---------------------------------------------------------------------------
+// Library-owned scratch for fdllm_kv_attn_fwd_noalloc: the same layout as a caller
+// workspace (counters, then (m, l) pairs, then partial rows), in a file-scope device
+// array, so the entry point allocates nothing. Every device that runs the library
+// holds its own copy at its own address until the process ends.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = static_cast<size_t>(FDLLM_KV_ATTN_SCRATCH_BYTES);
+static_assert(kScratchBytes > kCounterBytes, "scratch must hold the arrival counters");
+
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};  // device address of `scratch`, per device
+
+// Clears the arrival counters at the head of a device's scratch (a fill kernel, not a
+// memset node, so nothing but a kernel enters a stream).
+__global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// Device address of the current device's scratch. The first call on a device
+// resolves it with that device current and clears the counters on `stream`; it is
+// refused under stream capture, where the clearing kernel would only run at replay.
+int scratch_for_current_device(hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    set_last_error("fdllm_kv_attn_fwd_noalloc: hipGetDevice failed: %s", hipGetErrorString(e));
+    return static_cast<int>(e);
+  }
+  FDLLM_CHECK_ARG(dev >= 0 && dev < kMaxScratchDevices, "fdllm_kv_attn_fwd_noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    e = hipStreamIsCapturing(stream, &cs);
+    if (e != hipSuccess) {
+      set_last_error("fdllm_kv_attn_fwd_noalloc: hipStreamIsCapturing failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    if (cs != hipStreamCaptureStatusNone) {
+      set_last_error(
+          "fdllm_kv_attn_fwd_noalloc: the first call on device %d must not be under stream capture "
+          "(it clears the scratch counters); make one call before capturing",
+          dev);
+      return FDLLM_ERR_UNSUPPORTED;
+    }
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || ptr == nullptr) {
+      set_last_error("fdllm_kv_attn_fwd_noalloc: hipGetSymbolAddress(scratch) failed on device %d: %s", dev,
+                     hipGetErrorString(e));
+      return e != hipSuccess ? static_cast<int>(e) : FDLLM_ERR_UNSUPPORTED;
+    }
+    constexpr int kWords = static_cast<int>(kCounterBytes / sizeof(uint32_t));
+    zero_words_kernel<<<dim3((kWords + 255) / 256), dim3(256), 0, stream>>>(static_cast<uint32_t*>(ptr), kWords);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+      set_last_error("fdllm_kv_attn_fwd_noalloc: clearing the scratch failed: %s", hipGetErrorString(e));
+      return static_cast<int>(e);
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return FDLLM_OK;
+}
+
+}  // namespace
+}  // namespace fdllm
+
+extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  using namespace fdllm;
+  Plan pl;
+  const int rc = make_plan(d, &pl);
+  if (rc != FDLLM_OK) return rc;
+  return kv_attn_launch(d, pl, workspace, workspace_bytes, stream);
+}
+
+extern "C" int fdllm_kv_attn_fwd_noalloc(const fdllm_kv_attn_desc* d, void* stream) {
+  using namespace fdllm;
+  Plan pl;
+  int rc = make_plan(d, &pl);
+  if (rc != FDLLM_OK) return rc;
+  const size_t need = plan_workspace_bytes(d, pl);
+  if (need > kScratchBytes) {
+    set_last_error("fdllm_kv_attn_fwd_noalloc: this call needs %zu bytes of scratch, above the library's "
+                   "maximum of %zu (FDLLM_KV_ATTN_SCRATCH_BYTES); use fdllm_kv_attn_fwd with a workspace",
+                   need, kScratchBytes);
+    return FDLLM_ERR_WORKSPACE;
+  }
+  if (d->batch == 0 || d->q_len == 0) return FDLLM_OK;
+  void* ws = nullptr;
+  if (need > 0) {
+    rc = scratch_for_current_device(static_cast<hipStream_t>(stream), &ws);
+    if (rc != FDLLM_OK) return rc;
+  }
+  return kv_attn_launch(d, pl, ws, need > 0 ? kScratchBytes : 0, stream);
 }
 
 extern "C" int fdllm_kv_cache_write(const void* k_new, const void* v_new,

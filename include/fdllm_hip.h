@@ -183,6 +183,31 @@ int fdllm_kv_attn_workspace_size(const fdllm_kv_attn_desc* desc, size_t* bytes);
 int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* desc, void* workspace, size_t workspace_bytes,
                       void* stream);
 
+/* Bytes of the library's own attention scratch on each device (48 MiB). */
+#define FDLLM_KV_ATTN_SCRATCH_BYTES (48u * 1024u * 1024u)
+
+/* fdllm_kv_attn_fwd without a workspace argument and without any allocation: the
+ * split partials and arrival counters live in a device array of
+ * FDLLM_KV_ATTN_SCRATCH_BYTES that the library holds on every device it runs on
+ * until the process ends. Same kernels, same results as fdllm_kv_attn_fwd.
+ *
+ * No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc). It calls no hipMalloc / hipFree.
+ *   - A call whose fdllm_kv_attn_workspace_size exceeds FDLLM_KV_ATTN_SCRATCH_BYTES
+ *     is rejected with FDLLM_ERR_WORKSPACE (nothing launched). At head_dim 128 with
+ *     the automatic split (kv_split 0) the scratch holds any sub-block decode
+ *     (<= 64 query rows per KV head) of up to 64 sequences of at most 5120 keys
+ *     with <= 8 KV heads, and any full-block decode (<= 256 rows per KV head) of up
+ *     to 64 sequences of at most 10240 keys with <= 4 KV heads; calls that need no
+ *     workspace (prefill) always fit.
+ *   - The first call on a device resolves the scratch and clears its counters on
+ *     `stream`; it must not be made under stream capture (FDLLM_ERR_UNSUPPORTED).
+ *   - Every call on one device shares that device's scratch, and each call leaves
+ *     its counters at zero: calls on one stream run in order, but calls that overlap
+ *     in time on one device (other streams, other threads) race. */
+int fdllm_kv_attn_fwd_noalloc(const fdllm_kv_attn_desc* desc, void* stream);
+
 /* -------------------------------------------------------------------------
  * KV cache write: copy `num_tokens` new key/value rows of every sequence into
  * the (paged) cache at positions write_start[b] + t (or `write_offset` + t when
