@@ -20,6 +20,8 @@ import os
 # FDLLM_HIP_LIB overrides the location of the library (default: the in-tree build).
 LIB_PATH = Path(os.environ.get("FDLLM_HIP_LIB") or (Path(__file__).resolve().parent / "lib" / "libfdllm_hip.so"))
 
+ABI_VERSION = 2  # FDLLM_ABI_VERSION
+
 FDLLM_OK = 0
 FDLLM_ERR_INVALID_ARGUMENT = -1
 FDLLM_ERR_UNSUPPORTED = -2
@@ -60,6 +62,8 @@ class KVAttnDesc(ctypes.Structure):
         ("mask_mode", _c_i32), ("mask_block", _c_i32), ("dtype", _c_i32), ("kv_split", _c_i32),
         ("softmax_scale", _c_float),
         ("flags", _c_i32),
+        ("k_new", _c_vp), ("v_new", _c_vp),
+        ("new_stride_b", _c_i64), ("new_stride_s", _c_i64), ("new_stride_h", _c_i64),
     ]
 
 
@@ -154,7 +158,7 @@ def lib() -> ctypes.CDLL:
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
-        if handle.fdllm_abi_version() != 1:
+        if handle.fdllm_abi_version() != ABI_VERSION:
             raise RuntimeError("libfdllm_hip.so ABI version mismatch")
         _lib = handle
     return _lib

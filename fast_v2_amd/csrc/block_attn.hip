@@ -82,6 +82,12 @@ struct AttnParams {
   float2* ws_ml;     // [units, n_splits, rows_per_wg]
   int* ws_cnt;       // [units] arrival counters of the split decode kernel (zero between calls)
   int2* ws_unit;     // [units] (first slot, splits) written by the split prefill kernel for its merge
+  // fused cache write (prefill kernels): K / V rows of the Sq query tokens, [B, Sq, Hkv, D]
+  // with strides (n_sb, n_ss, n_sh), stored into the cache at positions qs + t below `cap`
+  const uint16_t* kn;
+  const uint16_t* vn;
+  int64_t n_sb, n_ss, n_sh;
+  int cap;
 };
 
 template <bool F16>
@@ -1326,7 +1332,16 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, c
 //     start first; workgroup ids of one (sequence, KV head) differ by a multiple
 //     of B * Hkv, which keeps its row blocks on one XCD (and its K/V in one L2)
 //     when B * Hkv is a multiple of 8.
-template <bool F16, bool PAGED, bool SPLIT>
+//   * FUSED: the call also stores the K / V rows of its query tokens (positions
+//     qs + t) into the cache. Keys at or past qs are read from those rows instead of
+//     the cache (so no workgroup reads a cache row this call writes), and each new row
+//     is stored by exactly one workgroup after its loop: the row block holding the
+//     last query row of its token (rows u G .. u G + G - 1 of token u), or the split
+//     whose key range holds it (the last split for rows past the visible length).
+//     The owned rows are the last keys the owner staged, so the copy reads them from
+//     the L2; stores inside the loop (from the staging registers) measured slower,
+//     because the extra address arithmetic and branches sat in every step.
+template <bool F16, bool PAGED, bool SPLIT, bool FUSED>
 __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) {
   constexpr int D = 128;
   constexpr int KT = 64;
@@ -1381,6 +1396,21 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
   const int row0 = rb * 256;
   const int ntiles = k_hi > k_lo ? (k_hi - k_lo + KT - 1) / KT : 0;
 
+  // FUSED: new rows at key positions [w_lo, w_hi) are this workgroup's to store
+  int w_lo = 0, w_hi = 0;
+  if constexpr (FUSED) {
+    const int qend = si.qs + p.Sq;
+    if constexpr (SPLIT) {
+      w_lo = max(k_lo, si.qs);
+      w_hi = split == n_act - 1 ? qend : min(k_hi, qend);
+    } else {
+      w_lo = si.qs + (256 * rb) / p.G;
+      w_hi = si.qs + min(p.Sq, (256 * (rb + 1)) / p.G);
+    }
+    w_lo = __builtin_amdgcn_readfirstlane(max(w_lo, 0));
+    w_hi = __builtin_amdgcn_readfirstlane(min(w_hi, p.cap));
+  }
+
   // ---- this lane's query row: Q^T fragments and key limit
   const int r = row0 + wave * 32 + n32;
   const int rc = min(r, p.R - 1);  // padding rows reuse a valid row: finite, never written
@@ -1425,8 +1455,96 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
   };
   Stage st0, st1;
 
+  // FUSED staging: per 32-key half, from the cache (keys before qs), from the new
+  // rows (keys from qs on), or, for the half that holds qs, one load per lane from its
+  // own row's source (rows past k_hi repeat row k_hi - 1, whose scores are masked).
+  const int hrow = tid >> 4;        // row of this thread's chunks within a 32-key half
+  const int hcol = (tid & 15) * 8;  // element column of the chunks
+  const uint16_t* knbase = FUSED ? p.kn + b * p.n_sb + kvh * p.n_sh : nullptr;
+  const uint16_t* vnbase = FUSED ? p.vn + b * p.n_sb + kvh * p.n_sh : nullptr;
+  const int nrow_bytes = FUSED ? static_cast<int>(p.n_ss) * 2 : 0;
+  // page of the 32-key half starting at kh (kh a multiple of 32, pages of >= 32 keys:
+  // every key of the half is on it); a uniform index, so a scalar load
+  auto half_page = [&](int kh) -> int {
+    if constexpr (PAGED) {
+      return pt_row[min(kh >> p.page_shift, p.max_pages - 1)];
+    } else {
+      return 0;
+    }
+  };
+  // element offset of key's row from kbase / vbase, given the page of its half
+  auto cache_off = [&](int page, int key, bool kcache) -> int64_t {
+    const int64_t ss = kcache ? p.k_ss : p.v_ss;
+    if constexpr (PAGED) {
+      return static_cast<int64_t>(page) * (kcache ? p.k_sp : p.v_sp) + (key & (p.page_size - 1)) * ss;
+    } else {
+      return static_cast<int64_t>(key) * ss;
+    }
+  };
+  auto load_half_fused = [&](Stage& sg, int i, int kh) {
+    const int valid = __builtin_amdgcn_readfirstlane(max(0, min(32, k_hi - kh)));
+    const int qs = si.qs;
+    const int page = half_page(kh);
+    if (kh < qs && qs < kh + 32 && valid > 0) {  // wave-uniform
+      // addresses of both sources, then one load per lane (same load count as below)
+      const int key = min(kh + hrow, k_hi - 1);
+      const uint16_t* kc = kbase + cache_off(page, key, true);
+      const uint16_t* vc = vbase + cache_off(page, key, false);
+      const uint16_t* kq = knbase + static_cast<int64_t>(key - qs) * p.n_ss;
+      const uint16_t* vq = vnbase + static_cast<int64_t>(key - qs) * p.n_ss;
+      const bool nw = key >= qs;
+      sg.k[i] = *reinterpret_cast<const u32x4*>((nw ? kq : kc) + hcol);
+      sg.v[i] = *reinterpret_cast<const u32x4*>((nw ? vq : vc) + hcol);
+      return;
+    }
+    const uint16_t* kp;
+    const uint16_t* vp;
+    int kbytes, vbytes;
+    if (kh >= qs) {
+      kp = knbase + static_cast<int64_t>(kh - qs) * p.n_ss;
+      vp = vnbase + static_cast<int64_t>(kh - qs) * p.n_ss;
+      kbytes = vbytes = nrow_bytes;
+    } else {
+      kp = kbase + cache_off(page, kh, true);
+      vp = vbase + cache_off(page, kh, false);
+      kbytes = krow_bytes;
+      vbytes = vrow_bytes;
+    }
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kp), 0, valid * kbytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vp), 0, valid * vbytes, kBufferFlags);
+    sg.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, hrow * kbytes + hcol * 2, 0, 0));
+    sg.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, hrow * vbytes + hcol * 2, 0, 0));
+  };
+  int noff[2];  // FUSED: byte offsets of this thread's chunks in a tile of new rows
+#pragma unroll
+  for (int i = 0; i < 2; ++i) noff[i] = (hrow + 32 * i) * nrow_bytes + hcol * 2;
   auto load_tile = [&](Stage& sg, int j) {
     const int kb = k_lo + j * KT;
+    if constexpr (FUSED) {
+      const int qs = si.qs;
+      if (kb >= qs) {  // wave-uniform: the whole tile is new rows (every tile of a plain prefill)
+        const int valid = __builtin_amdgcn_readfirstlane(max(0, min(KT, k_hi - kb)));
+        const int64_t noffs = static_cast<int64_t>(kb - qs) * p.n_ss;
+        const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(knbase + noffs), 0,
+                                                                            valid * nrow_bytes, kBufferFlags);
+        const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vnbase + noffs), 0,
+                                                                            valid * nrow_bytes, kBufferFlags);
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          sg.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, noff[i], 0, 0));
+          sg.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, noff[i], 0, 0));
+        }
+        return;
+      }
+      if (kb + KT > qs) {  // wave-uniform: the tile that holds qs, half by half
+        load_half_fused(sg, 0, kb);
+        load_half_fused(sg, 1, kb + 32);
+        return;
+      }
+      // otherwise every row of the tile is cached: the statement below
+    }
     if constexpr (PAGED) {
       if (p.page_size < KT) {
         // 32-key pages: chunk i of every thread lies in key half i of the tile
@@ -1583,6 +1701,22 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
       step(st1, j + 1);
     }
   }
+  if constexpr (FUSED) {
+    // the owned new rows into the cache: the ones the loop staged were read last, so
+    // these reads are served by the L2; rows past the visible length were never staged
+    const int c_lo = w_lo;
+    for (int c = tid; c < (w_hi - c_lo) * 16; c += 512) {
+      const int key = c_lo + (c >> 4);
+      const int col = (c & 15) * 8;
+      const int64_t src = static_cast<int64_t>(key - si.qs) * p.n_ss + col;
+      int page = 0;
+      if constexpr (PAGED) page = pt_row[min(key >> p.page_shift, p.max_pages - 1)];
+      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(kbase) + cache_off(page, key, true) + col) =
+          *reinterpret_cast<const u32x4*>(knbase + src);
+      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(vbase) + cache_off(page, key, false) + col) =
+          *reinterpret_cast<const u32x4*>(vnbase + src);
+    }
+  }
 
   // ---- epilogue: rows of both lane halves are whole after the exchange of l
   l_run = halves_sum(l_run);
@@ -1721,6 +1855,7 @@ struct KVWriteArgs {
   const int32_t* write_start;
   int write_offset;
   const int64_t* positions;
+  int pos_bias;  // added to write_start[b] / write_offset (the attention call's fallback write)
   int B, T, Hkv, D;
 };
 
@@ -1740,7 +1875,7 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const KVWriteArgs a) {
   if (a.positions) {
     pos = a.positions[static_cast<int64_t>(b) * a.T + t];
   } else {
-    pos = static_cast<int64_t>(a.write_start ? a.write_start[b] : a.write_offset) + t;
+    pos = static_cast<int64_t>(a.write_start ? a.write_start[b] : a.write_offset) + a.pos_bias + t;
   }
   int64_t off;
   if (a.page_table) {
@@ -1995,6 +2130,18 @@ void launch_combine(const AttnParams& p, unsigned units, hipStream_t s) {
   kv_attn_combine_kernel<D, F16, PAGED><<<cgrid, dim3(256), 0, s>>>(p);
 }
 
+template <bool SPLIT, bool FUSED>
+void launch_prefill(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
+  const bool paged = p.page_table != nullptr;
+  if (f16) {
+    if (paged) kv_prefill_kernel<true, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+    else kv_prefill_kernel<true, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+  } else {
+    if (paged) kv_prefill_kernel<false, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+    else kv_prefill_kernel<false, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+  }
+}
+
 template <int HKV>
 void launch_decode(const AttnParams& p, bool f16, hipStream_t s) {
   const bool paged = p.page_table != nullptr;
@@ -2136,6 +2283,22 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
   p.mask_mode = d->mask_mode;
   p.mask_block = d->mask_block > 0 ? d->mask_block : 1;
   p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
+  FDLLM_CHECK_ARG((d->k_new == nullptr) == (d->v_new == nullptr),
+                  "fdllm_kv_attn_fwd: k_new and v_new must both be given or both be NULL");
+  p.kn = static_cast<const uint16_t*>(d->k_new);
+  p.vn = static_cast<const uint16_t*>(d->v_new);
+  p.n_sb = d->new_stride_b;
+  p.n_ss = d->new_stride_s;
+  p.n_sh = d->new_stride_h;
+  p.cap = d->page_table ? static_cast<int>(std::min<int64_t>(static_cast<int64_t>(d->max_pages) * d->page_size,
+                                                              int64_t{1} << 30))
+                        : d->max_seqlen;
+  if (p.kn != nullptr) {
+    FDLLM_CHECK_ARG(aligned16(d->k_new) && aligned16(d->v_new) && d->new_stride_b % 8 == 0 &&
+                        d->new_stride_s % 8 == 0 && d->new_stride_h % 8 == 0,
+                    "fdllm_kv_attn_fwd: k_new / v_new must be 16-byte aligned with strides in multiples of 8");
+    FDLLM_CHECK_ARG(d->new_stride_s < (1 << 24), "fdllm_kv_attn_fwd: new_stride_s too large");
+  }
   if (need > 0) {
     char* w = static_cast<char*>(workspace);
     p.ws_cnt = reinterpret_cast<int*>(w);
@@ -2151,6 +2314,38 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
   }
   const bool f16 = d->dtype == FDLLM_DTYPE_F16;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  // Cache write of the call (k_new / v_new): inside the prefill kernels, otherwise as
+  // a kernel of its own before the attention, at q_start[b] + t (seqlens[b] - q_len + t)
+  const bool fuse_write = p.kn != nullptr && (pl.kind == kPlanPrefill || pl.kind == kPlanSplitPrefill);
+  if (p.kn != nullptr && !fuse_write) {
+    KVWriteArgs a;
+    a.k_new = p.kn;
+    a.v_new = p.vn;
+    a.n_sb = p.n_sb;
+    a.n_ss = p.n_ss;
+    a.n_sh = p.n_sh;
+    a.k_cache = const_cast<uint16_t*>(p.k);
+    a.v_cache = const_cast<uint16_t*>(p.v);
+    FDLLM_CHECK_ARG(p.k_sp == p.v_sp && p.k_ss == p.v_ss && p.k_sh == p.v_sh,
+                    "fdllm_kv_attn_fwd: a cache write with this shape needs equal K and V cache strides");
+    a.c_sp = p.k_sp;
+    a.c_ss = p.k_ss;
+    a.c_sh = p.k_sh;
+    a.page_table = p.page_table;
+    a.max_pages = p.max_pages;
+    a.page_size = p.page_size;
+    a.max_seqlen = p.max_seqlen;
+    a.write_start = p.q_start ? p.q_start : p.seqlens;
+    a.write_offset = 0;
+    a.positions = nullptr;
+    a.pos_bias = p.q_start ? 0 : -p.Sq;
+    a.B = p.B;
+    a.T = p.Sq;
+    a.Hkv = p.Hkv;
+    a.D = d->head_dim;
+    const int64_t n = static_cast<int64_t>(a.B) * a.T * a.Hkv * (a.D / 8);
+    kv_write_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(a);
+  }
   if (pl.kind == kPlanSplitDecode) {
     const bool paged = p.page_table != nullptr;
     const dim3 grid(pl.n_splits, d->num_kv_heads, pl.chunk > 0 ? d->batch : 1);
@@ -2164,27 +2359,15 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }
   if (pl.kind == kPlanPrefill) {
-    const bool paged = p.page_table != nullptr;
     const dim3 grid(static_cast<unsigned>(grid_z), pl.n_rb);
-    if (f16) {
-      if (paged) kv_prefill_kernel<true, true, false><<<grid, dim3(512), 0, s>>>(p);
-      else kv_prefill_kernel<true, false, false><<<grid, dim3(512), 0, s>>>(p);
-    } else {
-      if (paged) kv_prefill_kernel<false, true, false><<<grid, dim3(512), 0, s>>>(p);
-      else kv_prefill_kernel<false, false, false><<<grid, dim3(512), 0, s>>>(p);
-    }
+    if (fuse_write) launch_prefill<false, true>(p, f16, grid, s);
+    else launch_prefill<false, false>(p, f16, grid, s);
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }
   if (pl.kind == kPlanSplitPrefill) {
-    const bool paged = p.page_table != nullptr;
     const dim3 grid(pl.n_splits, d->num_kv_heads, pl.chunk > 0 ? d->batch : 1);
-    if (f16) {
-      if (paged) kv_prefill_kernel<true, true, true><<<grid, dim3(512), 0, s>>>(p);
-      else kv_prefill_kernel<true, false, true><<<grid, dim3(512), 0, s>>>(p);
-    } else {
-      if (paged) kv_prefill_kernel<false, true, true><<<grid, dim3(512), 0, s>>>(p);
-      else kv_prefill_kernel<false, false, true><<<grid, dim3(512), 0, s>>>(p);
-    }
+    if (fuse_write) launch_prefill<true, true>(p, f16, grid, s);
+    else launch_prefill<true, false>(p, f16, grid, s);
     if (p.ws_unit != nullptr) {
       // units = B * Hkv; 32 rows per workgroup
       const dim3 mgrid(static_cast<unsigned>((pl.R + 31) / 32), static_cast<unsigned>(d->batch * d->num_kv_heads));
@@ -2356,6 +2539,7 @@ extern "C" int fdllm_kv_cache_write(const void* k_new, const void* v_new,
   a.write_start = write_start;
   a.write_offset = write_offset;
   a.positions = positions;
+  a.pos_bias = 0;
   a.B = batch;
   a.T = num_tokens;
   a.Hkv = num_kv_heads;

@@ -169,7 +169,7 @@ def scatter_rows(values: torch.Tensor, indices: torch.Tensor,
 # ---------------------------------------------------------------------------
 
 def _attn_desc(q, k_cache, v_cache, seqlens, out, scale, mask_mode, mask_block,
-               q_start, page_table, page_size, kv_split, flags=0) -> _ffi.KVAttnDesc:
+               q_start, page_table, page_size, kv_split, flags=0, k_new=None, v_new=None) -> _ffi.KVAttnDesc:
     B, Sq, Hq, D = q.shape
     d = _ffi.KVAttnDesc()
     d.q = q.data_ptr()
@@ -199,6 +199,10 @@ def _attn_desc(q, k_cache, v_cache, seqlens, out, scale, mask_mode, mask_block,
     d.kv_split = int(kv_split)
     d.softmax_scale = float(scale)
     d.flags = int(flags)
+    if k_new is not None:
+        d.k_new = k_new.data_ptr()
+        d.v_new = v_new.data_ptr()
+        d.new_stride_b, d.new_stride_s, d.new_stride_h = k_new.stride(0), k_new.stride(1), k_new.stride(2)
     return d
 
 
@@ -217,6 +221,8 @@ def block_attn(
     kv_split: int = 0,
     decode_kernel: bool = True,
     all_heads_decode: bool = False,
+    k_new: Optional[torch.Tensor] = None,
+    v_new: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention of BSHD queries over a (paged) BSHD KV cache.
 
@@ -228,10 +234,24 @@ def block_attn(
     decode_kernel=False forces the general kernel where a decode kernel would
     apply; all_heads_decode=True picks the all-KV-heads decode kernel instead of
     the split-KV one (all compute the same function).
+    k_new / v_new [B, Sq, Hkv, D]: the K / V rows of the query tokens, stored into
+    the cache at positions q_start[b] + t (cache_seqlens[b] - Sq + t without q_start)
+    as part of the call, before any key is read (StaticKVCache.update followed by the
+    attention, static_kv_cache.py:132-160); the prefill kernels do it while staging.
     """
     if q.dim() != 4 or k_cache.dim() != 4 or v_cache.dim() != 4:
         raise RuntimeError("block_attn: q, k_cache and v_cache must be 4-D (BSHD)")
     tensors = [q, k_cache, v_cache, cache_seqlens]
+    if (k_new is None) != (v_new is None):
+        raise RuntimeError("block_attn: give k_new and v_new together")
+    if k_new is not None:
+        if k_new.shape != (q.shape[0], q.shape[1], k_cache.shape[2], q.shape[3]) or v_new.shape != k_new.shape:
+            raise RuntimeError(f"block_attn: k_new / v_new must be [B, Sq, Hkv, D]; got {tuple(k_new.shape)}")
+        if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+            raise RuntimeError("block_attn: k_new / v_new must have q's dtype")
+        if k_new.stride() != v_new.stride() or k_new.stride(-1) != 1:
+            k_new, v_new = k_new.contiguous(), v_new.contiguous()
+        tensors += [k_new, v_new]
     if q_start is not None:
         tensors.append(q_start)
     if page_table is not None:
@@ -271,7 +291,7 @@ def block_attn(
     desc = _attn_desc(q, k_cache, v_cache, cache_seqlens, out, softmax_scale, mask_mode,
                       mask_block, q_start, page_table, page_size, kv_split,
                       (0 if decode_kernel else _ffi.ATTN_NO_DECODE_KERNEL)
-                      | (_ffi.ATTN_ALL_HEADS_DECODE if all_heads_decode else 0))
+                      | (_ffi.ATTN_ALL_HEADS_DECODE if all_heads_decode else 0), k_new, v_new)
     L = _ffi.lib()
     need = ctypes.c_size_t(0)
     _ffi.check(L.fdllm_kv_attn_workspace_size(ctypes.byref(desc), ctypes.byref(need)),

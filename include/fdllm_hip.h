@@ -64,7 +64,7 @@ extern "C" {
 #define FDLLM_MASK_BLOCK_CAUSAL 2
 
 /* Library identification: returns FDLLM_ABI_VERSION. */
-#define FDLLM_ABI_VERSION 1
+#define FDLLM_ABI_VERSION 2
 int fdllm_abi_version(void);
 
 /* Human-readable description of the calling thread's last failure ("" if none). */
@@ -156,6 +156,20 @@ typedef struct fdllm_kv_attn_desc {
   int32_t kv_split;   /* keys per split-KV work item (multiple of 64), 0 = automatic */
   float softmax_scale;
   int32_t flags;      /* FDLLM_ATTN_* bits, 0 = defaults */
+  /* Optional cache write fused into the call (both NULL: none). k_new / v_new hold
+   * the key / value rows of the q_len query tokens, [batch, q_len, num_kv_heads,
+   * head_dim] with the strides below; row t of sequence b is stored into the cache
+   * (k / v, addressed as above) at position q_start[b] + t (seqlens[b] - q_len + t
+   * without q_start) before any key is read, positions outside [0, capacity) being
+   * skipped (capacity = max_pages * page_size with a page table, else max_seqlen).
+   * Replaces StaticKVCache.update (static_kv_cache.py:132-160) followed by the
+   * attention of the prefill / commit forward (modeling.py:385-411): the prefill
+   * kernels read these rows from k_new / v_new and store them from registers as they
+   * stage them, so the write costs no second read; other shapes launch the cache
+   * write kernel before the attention. */
+  const void* k_new;
+  const void* v_new;
+  int64_t new_stride_b, new_stride_s, new_stride_h;
 } fdllm_kv_attn_desc;
 
 /* Use the general kernel (one KV head per workgroup) even where the decode

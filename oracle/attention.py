@@ -12,6 +12,10 @@ sdpa_block_causal   the eager prefill / commit attention of
                     Fast_dLLM_QwenAttention.forward (modeling.py:385-411) with the
                     bool mask of eval_block_diff_mask / eval_mask
                     (modeling.py:145-150, :585-593) and repeat_kv (:202-211).
+cache_write_np      StaticKVCache.update's write (utils/static_kv_cache.py:132-160:
+                    rows t of the new K / V land at position start + t of the
+                    layer's buffer) generalised to per-sequence starts and the
+                    paged layout, with positions outside [0, capacity) skipped.
 attention_np        an independent float64 numpy brute force of
                     softmax(q k^T * scale + M) v covering every mask mode of the
                     HIP kernel and the paged KV layout. Rows with no visible key
@@ -81,6 +85,32 @@ def sdpa_block_causal(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, block_s
     mask = block_causal_mask(S, k.shape[1], block_size, past_len).to(q.device)
     out = F.scaled_dot_product_attention(qh, kh, vh, attn_mask=mask, is_causal=False, scale=scale)
     return out.transpose(1, 2).contiguous()
+
+
+def cache_write_np(cache: np.ndarray, new: np.ndarray, starts, page_table=None,
+                   page_size: Optional[int] = None, capacity: Optional[int] = None) -> np.ndarray:
+    """A copy of ``cache`` ([B, max_S, Hkv, D], or a page pool with ``page_table``)
+    with row t of ``new`` [B, T, Hkv, D] stored at position starts[b] + t, the
+    StaticKVCache.update write (utils/static_kv_cache.py:132-160) per sequence.
+    Positions < 0 or >= capacity (default: the buffer length, or pages x page_size)
+    are skipped."""
+    out = np.array(cache, copy=True)
+    new = np.asarray(new)
+    starts = np.asarray(starts).astype(np.int64)
+    B, T = new.shape[:2]
+    pt = None if page_table is None else np.asarray(page_table).astype(np.int64)
+    if capacity is None:
+        capacity = out.shape[1] if pt is None else pt.shape[1] * page_size
+    for b in range(B):
+        for t in range(T):
+            pos = int(starts[b]) + t
+            if pos < 0 or pos >= capacity:
+                continue
+            if pt is None:
+                out[b, pos] = new[b, t]
+            else:
+                out[pt[b, pos // page_size], pos % page_size] = new[b, t]
+    return out
 
 
 def gather_kv_np(cache: np.ndarray, b: int, length: int, page_table: Optional[np.ndarray],

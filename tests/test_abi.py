@@ -57,7 +57,7 @@ def test_ctypes_table_matches_header():
 
 
 def test_abi_version_and_error_string(lib):
-    assert lib.fdllm_abi_version() == 1
+    assert lib.fdllm_abi_version() == 2
     assert isinstance(lib.fdllm_last_error(), bytes)
 
 

@@ -150,16 +150,24 @@ def test_block_causal_prefill_with_cache_write(gpu):
 
 
 def test_block_causal_prefill_full_size_sampled(gpu):
-    """4 x 4096 block-causal prefill; sampled query blocks checked against the brute force."""
+    """4 x 4096 block-causal prefill with the K/V cache write fused into the call (the
+    benchmarked config): the cache holds the new rows bit for bit, the output equals the
+    separate write + attention bit for bit, and sampled query blocks match the brute force."""
     wl = workloads.block_prefill(seed=0)
     B, S, Hkv, D = wl.k.shape
-    kc = torch.empty(B, S, Hkv, D, dtype=torch.bfloat16, device=gpu)
-    vc = torch.empty_like(kc)
-    ops.kv_cache_write(wl.k.to(gpu), wl.v.to(gpu), kc, vc)
+    kc = torch.full((B, S, Hkv, D), 7.0, dtype=torch.bfloat16, device=gpu)
+    vc = torch.full_like(kc, -7.0)
     seqlens = torch.full((B,), S, dtype=torch.int32, device=gpu)
+    k, v = wl.k.to(gpu), wl.v.to(gpu)
     out = ops.block_attn(wl.q.to(gpu), kc, vc, seqlens, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL,
-                         mask_block=wl.block).cpu()
-    assert torch.equal(kc.cpu(), wl.k)
+                         mask_block=wl.block, k_new=k, v_new=v)
+    assert torch.equal(kc, k) and torch.equal(vc, v)
+    ku, vu = torch.empty_like(kc), torch.empty_like(vc)
+    ops.kv_cache_write(k, v, ku, vu)
+    ref = ops.block_attn(wl.q.to(gpu), ku, vu, seqlens, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL,
+                         mask_block=wl.block)
+    assert torch.equal(out, ref)
+    out = out.cpu()
     for blk in (0, 1, 63, 64, 127):
         t0 = blk * wl.block
         qs = torch.full((B,), t0, dtype=torch.int32)
@@ -547,3 +555,80 @@ def test_block_decode_split_prefill_kernel(gpu, case):
         out = ops.block_attn(q.to(gpu), kc.to(gpu), vc.to(gpu), sl.to(gpu), scale, kv_split=split,
                              decode_kernel=dk, **args)
         _check(out, exp)
+
+
+@pytest.mark.parametrize("case", [
+    "prefill_q0_contig",        # 4 KV heads x 4200 rows: prefill kernel, every key new
+    "prefix_paged32_mixed",     # cached prefix ending inside a 32-key half (per-lane sources)
+    "prefix_paged64_fp16",      # fp16, 64-key pages, prefix on a page boundary
+    "commit_split_paged32",     # a whole 32-token block per sequence: split prefill kernel
+    "commit_split_misaligned",  # the same with prefixes that are not multiples of 32
+    "short_visible_qstart",     # new rows past the visible length: copied after the loop
+    "past_capacity",            # new rows past the cache's end are dropped
+    "subblock_fallback",        # 8 queries: split decode kernel, cache write kernel first
+    "head64_fallback",          # head_dim 64: the general kernel, cache write kernel first
+])
+def test_fused_cache_write(gpu, case):
+    """k_new / v_new: the call stores the query tokens' K / V rows into the cache at
+    q_start + t and attends over the updated cache. The cache must equal the oracle's
+    write bit for bit, the output must equal the same call made as a separate cache
+    write followed by the attention (bit for bit) and match the float64 oracle over
+    the written cache."""
+    g = torch.Generator().manual_seed(sum(map(ord, case)))
+    dtype, page, mode, blk, D, hq, hkv, explicit_qs = torch.bfloat16, 0, _ffi.MASK_BLOCK_CAUSAL, 32, 128, 28, 4, False
+    if case == "prefill_q0_contig":
+        B, Sq, qs, cap, lens = 2, 600, [0, 0], 700, None
+    elif case == "prefix_paged32_mixed":
+        B, Sq, qs, cap, lens, page = 2, 400, [45, 130], 640, None, 32
+    elif case == "prefix_paged64_fp16":
+        B, Sq, qs, cap, lens, page, dtype = 2, 400, [64, 192], 640, None, 64, torch.float16
+    elif case == "commit_split_paged32":
+        B, Sq, qs, cap, lens, page = 5, 32, [1024, 64, 0, 2016, 320], 2112, None, 32
+    elif case == "commit_split_misaligned":
+        B, Sq, qs, cap, lens = 5, 32, [1000, 77, 5, 0, 2049], 2112, None
+    elif case == "short_visible_qstart":
+        B, Sq, qs, cap, lens, mode, explicit_qs = 2, 400, [96, 10], 600, [446, 330], _ffi.MASK_SEQLEN, True
+    elif case == "past_capacity":
+        B, Sq, qs, cap, lens, explicit_qs = 1, 600, [100], 650, [650], True
+    elif case == "subblock_fallback":
+        B, Sq, qs, cap, lens, page = 4, 8, [1000, 500, 64, 2047], 2112, None, 32
+    else:
+        B, Sq, qs, cap, lens, D, hq, hkv = 3, 300, [0, 33, 128], 512, None, 64, 8, 2
+    if lens is None:
+        lens = [q0 + Sq for q0 in qs]
+    print(f"case fused cache write {case}", flush=True)
+    q = torch.randn(B, Sq, hq, D, generator=g).to(dtype)
+    kc0 = torch.randn(B, cap, hkv, D, generator=g).to(dtype)
+    vc0 = torch.randn(B, cap, hkv, D, generator=g).to(dtype)
+    kn = torch.randn(B, Sq, hkv, D, generator=g).to(dtype)
+    vn = torch.randn(B, Sq, hkv, D, generator=g).to(dtype)
+    sl = torch.tensor(lens, dtype=torch.int32)
+    qst = torch.tensor(qs, dtype=torch.int32)
+    if page:
+        kp0, vp0, pt = _paginate(kc0, vc0, page, g)
+        args = dict(page_table=pt.to(gpu), page_size=page)
+    else:
+        kp0, vp0, pt, args = kc0, vc0, None, {}
+    exp_k = oa.cache_write_np(kp0.numpy() if dtype == torch.float16 else kp0.view(torch.int16).numpy(),
+                              kn.numpy() if dtype == torch.float16 else kn.view(torch.int16).numpy(), qs,
+                              page_table=pt, page_size=page or None, capacity=cap)
+    exp_v = oa.cache_write_np(vp0.numpy() if dtype == torch.float16 else vp0.view(torch.int16).numpy(),
+                              vn.numpy() if dtype == torch.float16 else vn.view(torch.int16).numpy(), qs,
+                              page_table=pt, page_size=page or None, capacity=cap)
+    qarg = dict(q_start=qst.to(gpu)) if explicit_qs else {}
+    kf, vf = kp0.to(gpu), vp0.to(gpu)
+    out = ops.block_attn(q.to(gpu), kf, vf, sl.to(gpu), mask_mode=mode, mask_block=blk, k_new=kn.to(gpu),
+                         v_new=vn.to(gpu), **qarg, **args)
+    as_np = (lambda t: t.cpu().numpy()) if dtype == torch.float16 else (lambda t: t.cpu().view(torch.int16).numpy())
+    assert np.array_equal(as_np(kf), exp_k), "K cache differs from the oracle's write"
+    assert np.array_equal(as_np(vf), exp_v), "V cache differs from the oracle's write"
+    # the unfused statement: the cache write kernel, then the attention
+    ku, vu = kp0.to(gpu), vp0.to(gpu)
+    ops.kv_cache_write(kn.to(gpu), vn.to(gpu), ku, vu, write_start=qst.to(gpu), **args)
+    ref = ops.block_attn(q.to(gpu), ku, vu, sl.to(gpu), mask_mode=mode, mask_block=blk, **qarg, **args)
+    assert torch.equal(ku, kf) and torch.equal(vu, vf)
+    assert torch.equal(out, ref), "fused call differs from write + attention"
+    kx = torch.from_numpy(exp_k).view(dtype) if dtype != torch.float16 else torch.from_numpy(exp_k)
+    vx = torch.from_numpy(exp_v).view(dtype) if dtype != torch.float16 else torch.from_numpy(exp_v)
+    _check(out, oa.attention_np(q.float(), kx.float(), vx.float(), torch.clamp(sl, max=cap), mask_mode=mode,
+                                mask_block=blk, q_start=qst, page_table=pt, page_size=page or None))

@@ -258,3 +258,36 @@ def test_e2e_oracle_attention_variants():
     assert 0 < (lo - ref).abs().max() < 2e-2
     # one visible key: p = 1 exactly in bf16, so both variants return that value row
     torch.testing.assert_close(lo[2], v[2, 0].repeat_interleave(4, 0)[None].expand(5, 8, 32), atol=0, rtol=0)
+
+
+def test_cache_write_matches_slice_assignment_and_paging():
+    """cache_write_np against torch slice assignment (the StaticKVCache.update
+    statement, static_kv_cache.py:132-160, one start per sequence), the paged layout
+    against the contiguous one, and the capacity rule; a planted off-by-one start
+    fails."""
+    g = torch.Generator().manual_seed(3)
+    B, S, Hkv, D, T = 3, 96, 2, 8, 20
+    cache = torch.randn(B, S, Hkv, D, generator=g)
+    new = torch.randn(B, T, Hkv, D, generator=g)
+    starts = [0, 37, 86]  # the last one runs past the capacity: rows 96.. are dropped
+    exp = cache.clone()
+    for b, s0 in enumerate(starts):
+        n = min(T, S - s0)
+        exp[b, s0:s0 + n] = new[b, :n]
+    got = oa.cache_write_np(cache.numpy(), new.numpy(), starts)
+    assert np.array_equal(got, exp.numpy())
+    assert np.array_equal(got[2, 86:], new[2, :10].numpy())
+    planted = oa.cache_write_np(cache.numpy(), new.numpy(), [s + 1 for s in starts])
+    assert not np.array_equal(planted, exp.numpy())
+    # paged: shuffled 32-key pages hold the same rows after the same write
+    ps, per = 32, S // 32
+    perm = torch.randperm(B * per, generator=g)
+    pt = perm.view(B, per).numpy()
+    pool = np.zeros((B * per, ps, Hkv, D), dtype=np.float32)
+    for b in range(B):
+        for i in range(per):
+            pool[pt[b, i]] = cache[b, i * ps:(i + 1) * ps].numpy()
+    pool2 = oa.cache_write_np(pool, new.numpy(), starts, page_table=pt, page_size=ps)
+    for b in range(B):
+        back = np.concatenate([pool2[pt[b, i]] for i in range(per)], axis=0)
+        assert np.array_equal(back, exp[b].numpy())
