@@ -204,12 +204,10 @@ def bench_decode_full(torch, args):
     return res
 
 
-def cpu_baseline_decode(torch, wl, seconds: float):
+def cpu_baseline_decode(torch, wl):
     """Reference CPU path (SDPA shim) on the same bs16 inputs, bf16, contiguous static cache."""
     from oracle import attention as oa
 
-    n = len(os.sched_getaffinity(0))
-    torch.set_num_threads(n)
     B, Sq, Hq, D = wl.q.shape
     Hkv = wl.k_pool.shape[-2]
     max_s = int(wl.seqlens.max())
@@ -222,18 +220,9 @@ def cpu_baseline_decode(torch, wl, seconds: float):
         pages = wl.page_table[b, pos // wl.page_size].long()
         k[b, :L] = layer_k[pages, pos % wl.page_size]
         v[b, :L] = layer_v[pages, pos % wl.page_size]
-    oa.sdpa_kvcache(wl.q, k, v, wl.seqlens, scaling=wl.scale)  # warm
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < 3:
-        t0 = time.perf_counter()
-        oa.sdpa_kvcache(wl.q, k, v, wl.seqlens, scaling=wl.scale)
-        times.append(time.perf_counter() - t0)
-    med = statistics.median(times) * 1e6
-    return {"value": round(med, 1), "unit": "us/step", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": (f"SDPA shim (tests/test_focus.py:205-228 restated in oracle/attention.py), bf16, "
-                       f"the full bs16 batch of one layer, contiguous [16, {max_s}, 4, 128] cache; "
-                       f"median of {len(times)} calls over ~{seconds:.0f} s")}
+    st = _cpu_protocol(torch, lambda: oa.sdpa_kvcache(wl.q, k, v, wl.seqlens, scaling=wl.scale))
+    return _cpu_result(st, "us/step", f"SDPA shim (tests/test_focus.py:205-228 restated in oracle/attention.py), "
+                       f"bf16, the full bs16 batch of one layer, contiguous [16, {max_s}, 4, 128] cache")
 
 
 # ---------------------------------------------------------------------------
@@ -262,7 +251,30 @@ def bench_gather(torch, args):
         res[name] = {"us_per_call": us, "bytes_per_call": nbytes, "achieved_gbs": gbs,
                      "roofline": _roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s",
                                            _traffic(f"gather_rmsnorm_{name}"))}
-    del hs
+    # The practical ceiling of a call this size, timed the same way (graph of the same
+    # number of nodes, inputs rotated through the same 48 HBM-resident slabs): a plain
+    # device copy of the bytes the gather moves (the 1024 x 3584 rows read and written,
+    # torch's copy kernel), and an empty kernel node (torch.cuda._sleep(0)).
+    T, H = idx.shape[1], wl.hidden.shape[2]
+    src = [h[0, :T] for h in hs]
+    dst = torch.empty((T, H), dtype=wl.hidden.dtype, device=dev)
+
+    def copy_step(i):
+        dst.copy_(src[i % copies])
+
+    us_copy = _time_graph(torch, copy_step, args.gather_steps, min(args.warmup, 32))
+    us_empty = _time_graph(torch, lambda i: torch.cuda._sleep(0), args.gather_steps, min(args.warmup, 32))
+    copy_bytes = 2 * T * H * 2
+    res["ceiling"] = {
+        "copy_us_per_call": us_copy, "copy_bytes": copy_bytes,
+        "copy_gbs": copy_bytes / (us_copy * 1e-6) / 1e9,
+        "empty_kernel_us_per_node": us_empty,
+        "normed_vs_copy": res["normed"]["us_per_call"] / us_copy,
+        "note": ("plain copy of the 1024 x 3584 bf16 rows (read + write, the normed call's bytes less "
+                 "the 15 KB of weight and indices) and an empty kernel node, each as a graph of the same "
+                 "length as the gather's"),
+    }
+    del hs, src, dst
     torch.cuda.empty_cache()
     return res
 
@@ -361,7 +373,10 @@ def bench_e2e(torch, args):
            "params": em.param_count(cfg), "model_build_s": round(build_s, 2),
            "gemm_tuning": "torch TunableOp over hipBLASLt / rocBLAS solutions, tuned in the warm-up",
            "forwards_graphed": "diffusion steps replayed from HIP graphs; commits eager",
-           "weights": args.e2e_weights or "random init (N(0, 0.02))",
+           "weights": args.e2e_weights or ("random init (N(0, 0.02), zero biases, unit norms) except the mask "
+                                           "token's lm_head row, which is zero: a random model may otherwise "
+                                           "predict the mask token, which the unmask rule writes back, and the "
+                                           "block never completes"),
            "config": "28 layers, hidden 3584, 28/4 heads, vocab 152064, bf16; batch 16, prompt 512, "
                      f"{args.e2e_tokens} new tokens, block 32, sub-block 8, threshold 0.9 (p > 0.9), block cache on"}
     del model, out, x
@@ -388,50 +403,128 @@ def calibrate_copies(torch):
     return res
 
 
-def _cpu_median_us(fn, seconds: float, min_calls: int = 3):
-    fn()  # warm
-    times = []
-    t_end = time.perf_counter() + seconds
-    while time.perf_counter() < t_end or len(times) < min_calls:
+def _cpu_protocol(torch, fn, warmup: int = 10, measured: int = 50):
+    """The reference's timing protocol (tests/bench_compile.py:179-214): `warmup`
+    untimed calls, then `measured` timed ones; median and the mean after dropping the
+    fastest and slowest 10 %. Threads: every core this process may run on."""
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    for _ in range(warmup):
+        fn()
+    lat = []
+    for _ in range(measured):
         t0 = time.perf_counter()
         fn()
-        times.append(time.perf_counter() - t0)
-    return statistics.median(times) * 1e6, len(times)
+        lat.append(time.perf_counter() - t0)
+    lat.sort()
+    trim = max(1, len(lat) // 10)
+    kept = lat[trim:-trim]
+    return {"median_us": round(lat[len(lat) // 2] * 1e6, 1),
+            "trimmed_mean_us": round(sum(kept) / len(kept) * 1e6, 1),
+            "warmup": warmup, "measured": measured, "cores": torch.get_num_threads()}
 
 
-def cpu_baseline_gather(torch, seconds: float):
+def _cpu_result(st, unit: str, sample: str, scale: float = 1.0):
+    """cpu_baseline object: value = median x scale (the sample's share of the workload)."""
+    return {"value": round(st["median_us"] * scale, 1), "unit": unit, "cores": st["cores"], "kind": "port",
+            "median_us_sample": st["median_us"], "trimmed_mean_us_sample": st["trimmed_mean_us"],
+            "protocol": f"{st['warmup']} warm-up + {st['measured']} timed calls; median, 10 %-trimmed mean",
+            "sample": sample}
+
+
+def cpu_baseline_gather(torch):
     """Reference CPU path for gather + RMSNorm: ref_gather_input_rmsnorm
     (cuda_bench/test_correctness.py:33-50) on the full bf16 [4096 x 3584] / 1024-row call."""
     from fast_v2_amd import workloads
     from oracle import gather_rmsnorm as og
 
-    n = len(os.sched_getaffinity(0))
-    torch.set_num_threads(n)
     wl = workloads.gather_rmsnorm_rows(seed=0)
-    us, calls = _cpu_median_us(lambda: og.ref_gather_input_rmsnorm(wl.hidden, wl.indices, wl.weight, wl.eps), seconds)
-    return {"value": round(us, 1), "unit": "us/call", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": (f"ref_gather_input_rmsnorm (cuda_bench/test_correctness.py:33-50 restated in "
-                       f"oracle/gather_rmsnorm.py), the whole call (gathered + normed outputs); median of "
-                       f"{calls} calls over ~{seconds:.0f} s")}
+    st = _cpu_protocol(torch, lambda: og.ref_gather_input_rmsnorm(wl.hidden, wl.indices, wl.weight, wl.eps))
+    return _cpu_result(st, "us/call", "ref_gather_input_rmsnorm (cuda_bench/test_correctness.py:33-50 restated in "
+                       "oracle/gather_rmsnorm.py), the whole call (gathered + normed outputs)")
 
 
-def cpu_baseline_prefill(torch, seconds: float):
+def cpu_baseline_prefill(torch):
     """Reference CPU path for block-causal prefill: SDPA with the block-causal bool mask
     (modeling.py:145-150, :398-411) on sequence 0 of the 4; value = 4 x that time."""
     from fast_v2_amd import workloads
     from oracle import attention as oa
 
-    n = len(os.sched_getaffinity(0))
-    torch.set_num_threads(n)
     wl = workloads.block_prefill(seed=0)
     q, k, v = wl.q[:1], wl.k[:1], wl.v[:1]
-    us, calls = _cpu_median_us(lambda: oa.sdpa_block_causal(q, k, v, wl.block, scaling=wl.scale), seconds,
-                               min_calls=2)
-    return {"value": round(4 * us, 1), "unit": "us/call", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": (f"SDPA with the block-causal mask (oracle/attention.py sdpa_block_causal), bf16, "
-                       f"sequence 0 of the 4 ([1, 4096, 28, 128] against 4 KV heads): median {us:.0f} us "
-                       f"over {calls} calls in ~{seconds:.0f} s; value = 4 x the sample (the sequences "
-                       f"are the same size)")}
+    st = _cpu_protocol(torch, lambda: oa.sdpa_block_causal(q, k, v, wl.block, scaling=wl.scale))
+    return _cpu_result(st, "us/call", "SDPA with the block-causal mask (oracle/attention.py sdpa_block_causal), "
+                       "bf16, sequence 0 of the 4 ([1, 4096, 28, 128] against 4 KV heads); value = 4 x the "
+                       "sample's median (the sequences are the same size)", scale=4.0)
+
+
+def cpu_baseline_small_fp32(torch):
+    """Config 1 on the CPU: the SDPA shim in fp32, batch 1, 12 / 2 heads, 512 prefix + 32
+    block keys, 32 queries (the reference's only CPU statement of the kv-cache attention)."""
+    from fast_v2_amd import workloads
+    from oracle import attention as oa
+
+    wl = workloads.kv_decode_fp32_small(seed=0)
+    st = _cpu_protocol(torch, lambda: oa.sdpa_kvcache(wl.q, wl.k_cache, wl.v_cache, wl.seqlens, scaling=wl.scale))
+    flops = 4 * 32 * 12 * 128 * 544
+    res = _cpu_result(st, "us/call", "SDPA shim (tests/test_focus.py:205-228 restated in oracle/attention.py), "
+                      "fp32, q [1, 32, 12, 128] over 544 keys of 2 KV heads, the whole call")
+    res["gflops"] = round(flops / (st["median_us"] * 1e-6) / 1e9, 2)
+    return res
+
+
+def cpu_baseline_e2e_step(torch):
+    """Config 5 on the CPU (the whole 7B model at batch 16 does not fit a bounded sample):
+    one decoder layer of the random-init 7B-layout model running a sub-block diffusion
+    step (16 sequences x 8 tokens at positions 512..519, attention over the 512-token
+    prompt plus the 32-token block through the SDPA shim, the reference's eager path
+    restated in oracle/e2e_eager.py), and the lm_head over the same 128 rows; value =
+    28 x layer + lm_head, an extrapolation from the two timed pieces."""
+    from fast_v2_amd.e2e import model as em
+    from oracle.e2e_eager import TorchKVCache, eager_attention_forward
+
+    cfg = em.BlockDiffusionConfig()
+    B, S, P = 16, 8, 512
+    g = torch.Generator().manual_seed(0)
+    dt = torch.bfloat16
+    with torch.no_grad():
+        layer = em.DecoderLayer(cfg, 0).to(dt)
+        for mod in layer.modules():
+            if isinstance(mod, torch.nn.Linear):
+                mod.weight.normal_(0.0, cfg.initializer_range, generator=g)
+                if mod.bias is not None:
+                    mod.bias.zero_()
+        lm_head = torch.nn.Linear(cfg.hidden_size, cfg.vocab_size, bias=False).to(dt)
+        lm_head.weight.normal_(0.0, cfg.initializer_range, generator=g)
+    layer.self_attn.forward = eager_attention_forward(layer.self_attn, False)
+    cache = TorchKVCache(B, P + 64, 1, cfg.num_key_value_heads, cfg.head_dim, dt, "cpu")
+    cache.key_cache[0].normal_(generator=g)
+    cache.value_cache[0].normal_(generator=g)
+    cache.set_kv_write_start(P)
+    cache.set_scratch_seqlens(P + cfg.bd_size)
+    h = torch.randn(B, S, cfg.hidden_size, generator=g).to(dt)
+    d = cfg.head_dim
+    inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    freqs = torch.arange(P, P + S).float()[:, None] * inv_freq[None, :]
+    emb = torch.cat((freqs, freqs), dim=-1)
+    pe = (emb.cos().to(dt)[None], emb.sin().to(dt)[None])
+
+    def run_layer():
+        with torch.no_grad():
+            layer(h, pe, cache, False, None, None)
+
+    def run_head():
+        with torch.no_grad():
+            lm_head(h)
+    st_l = _cpu_protocol(torch, run_layer)
+    st_h = _cpu_protocol(torch, run_head)
+    per_step = cfg.num_hidden_layers * st_l["median_us"] + st_h["median_us"]
+    tokens_per_s = B / (per_step * 1e-6)  # at least one token per sequence per step
+    return {"value": round(per_step, 1), "unit": "us/diffusion step (extrapolated)", "cores": st_l["cores"],
+            "kind": "port", "layer": st_l, "lm_head": st_h,
+            "tokens_per_s_at_one_token_per_row_per_step": round(tokens_per_s, 2),
+            "sample": ("one decoder layer (eager torch + SDPA shim, bf16) on a 16 x 8-token sub-block step "
+                       "over 544 visible keys, and the lm_head on the same 128 rows; value = 28 x layer median "
+                       "+ lm_head median (extrapolated to the 28-layer model; embedding and final norm left out)")}
 
 
 # ---------------------------------------------------------------------------
@@ -448,7 +541,6 @@ def main() -> int:
                     help="KV layout: 32-token pages, the contiguous [B, max_S, Hkv, D] static cache, "
                          "or the same cache stored head-major")
     ap.add_argument("--no-check", action="store_true", help="skip the graph-vs-eager equality check")
-    ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["decode", "decode_full", "gather", "prefill", "e2e"], default=None)
     ap.add_argument("--e2e-tokens", type=int, default=1024, help="tokens generated in the end-to-end leg")
@@ -499,7 +591,10 @@ def main() -> int:
              f"{extra['block_decode_full']['achieved_gbs']:.0f} GB/s, {extra['block_decode_full']['tflops']:.0f} TFLOP/s")
     if args.only in (None, "gather"):
         extra["gather_rmsnorm"] = bench_gather(torch, args)
-        _log(f"gather: {json.dumps({k: round(v['us_per_call'], 3) for k, v in extra['gather_rmsnorm'].items()})} us")
+        g = extra["gather_rmsnorm"]
+        _log(f"gather: normed {g['normed']['us_per_call']:.3f} us, pair {g['pair']['us_per_call']:.3f} us; "
+             f"plain copy of the rows {g['ceiling']['copy_us_per_call']:.3f} us, empty kernel node "
+             f"{g['ceiling']['empty_kernel_us_per_node']:.3f} us")
     if args.only in (None, "prefill"):
         extra["prefill"] = bench_prefill(torch, args)
         _log(f"prefill: {extra['prefill']['us_per_call']:.1f} us per call with the cache write, "
@@ -512,14 +607,20 @@ def main() -> int:
 
     cpu = None
     if decode is not None and not args.no_cpu_baseline:
-        _log("cpu baseline ...")
-        cpu = cpu_baseline_decode(torch, wl, args.cpu_seconds)
+        _log("cpu baseline (decode, config 3) ...")
+        cpu = cpu_baseline_decode(torch, wl)
+        _log("cpu baseline (config 1, fp32 SDPA) ...")
+        extra["small_fp32_cpu"] = cpu_baseline_small_fp32(torch)
     if not args.no_cpu_baseline:
         if "gather_rmsnorm" in extra:
-            extra["gather_rmsnorm"]["cpu_baseline"] = cpu_baseline_gather(torch, min(args.cpu_seconds, 5.0))
+            _log("cpu baseline (gather + RMSNorm) ...")
+            extra["gather_rmsnorm"]["cpu_baseline"] = cpu_baseline_gather(torch)
         if "prefill" in extra:
             _log("cpu baseline (prefill sample) ...")
-            extra["prefill"]["cpu_baseline"] = cpu_baseline_prefill(torch, args.cpu_seconds)
+            extra["prefill"]["cpu_baseline"] = cpu_baseline_prefill(torch)
+        if "e2e" in extra:
+            _log("cpu baseline (end-to-end diffusion step, one layer + lm_head) ...")
+            extra["e2e"]["cpu_baseline"] = cpu_baseline_e2e_step(torch)
 
     if decode is not None:
         us = decode["us_per_step"]

@@ -56,6 +56,11 @@ constexpr int kMaxDecodeSplits = 16;  // key splits per (sequence, KV head) in t
 #define FDLLM_DECODE_STAGES 2
 #endif
 constexpr int kDecodeStages = FDLLM_DECODE_STAGES;  // tiles in flight per workgroup in the split decode kernel
+// Waves (x 32 query rows) per prefill workgroup. Measured and not kept: 4 waves (two
+// independent workgroups per CU, so that their softmax and MFMA phases drift apart):
+// 549 us against 516-523 us for the 4 x 4096 prefill, the doubled K/V staging per
+// thread pushed it to 256 VGPRs with spills.
+constexpr int kPrefillWaves = 8;
 
 struct AttnParams {
   const uint16_t* q;
@@ -1335,16 +1340,22 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, c
 //   * FUSED: the call also stores the K / V rows of its query tokens (positions
 //     qs + t) into the cache. Keys at or past qs are read from those rows instead of
 //     the cache (so no workgroup reads a cache row this call writes), and each new row
-//     is stored by exactly one workgroup after its loop: the row block holding the
+//     is stored by exactly one workgroup before its loop: the row block holding the
 //     last query row of its token (rows u G .. u G + G - 1 of token u), or the split
-//     whose key range holds it (the last split for rows past the visible length).
-//     The owned rows are the last keys the owner staged, so the copy reads them from
-//     the L2; stores inside the loop (from the staging registers) measured slower,
-//     because the extra address arithmetic and branches sat in every step.
-template <bool F16, bool PAGED, bool SPLIT, bool FUSED>
-__global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) {
+//     whose key range holds it (the last split for rows past the visible length). The
+//     copy's loads are issued with the first tiles' and share their wait. Measured and
+//     not kept: stores from the staging registers inside the loop (the address
+//     arithmetic and branches sat in every step), and the copy after the loop (its
+//     load latency then sat at the end of every workgroup).
+template <bool F16, bool PAGED, bool SPLIT, bool FUSED, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void kv_prefill_kernel(const AttnParams p) {
   constexpr int D = 128;
   constexpr int KT = 64;
+  constexpr int NT = 64 * NW;      // threads
+  constexpr int ROWS = 32 * NW;    // query rows per workgroup
+  constexpr int CPT = 1024 / NT;   // 16-byte chunks of a K (or V) tile per thread
+  constexpr int RPS = NT / 16;     // key rows covered by one chunk index
+  static_assert(NW == 8 || (NW == 4 && !SPLIT), "split mode keeps 256 rows per workgroup");
   constexpr int KS = D + 8;  // K row stride in LDS: 16-byte pad
   // V in two regions, columns 32 d + [0, 16) in the first and 32 d + [16, 32) in the
   // second (row stride 80 elements each), the second shifted by 128 bytes past the
@@ -1393,7 +1404,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
     n_act = 1;
     split = first = 0;
   }
-  const int row0 = rb * 256;
+  const int row0 = rb * ROWS;
   const int ntiles = k_hi > k_lo ? (k_hi - k_lo + KT - 1) / KT : 0;
 
   // FUSED: new rows at key positions [w_lo, w_hi) are this workgroup's to store
@@ -1404,8 +1415,8 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
       w_lo = max(k_lo, si.qs);
       w_hi = split == n_act - 1 ? qend : min(k_hi, qend);
     } else {
-      w_lo = si.qs + (256 * rb) / p.G;
-      w_hi = si.qs + min(p.Sq, (256 * (rb + 1)) / p.G);
+      w_lo = si.qs + (ROWS * rb) / p.G;
+      w_hi = si.qs + min(p.Sq, (ROWS * (rb + 1)) / p.G);
     }
     w_lo = __builtin_amdgcn_readfirstlane(max(w_lo, 0));
     w_hi = __builtin_amdgcn_readfirstlane(min(w_hi, p.cap));
@@ -1436,13 +1447,13 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
     for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
   float m_run = -INFINITY, l_run = 0.f;
 
-  // ---- staging: chunk c = tid + 512 i of a tile is key c / 16, 16-byte column c % 16
+  // ---- staging: chunk c = tid + NT i of a tile is key c / 16, 16-byte column c % 16
   const int krow_bytes = static_cast<int>(p.k_ss) * 2;
   const int vrow_bytes = static_cast<int>(p.v_ss) * 2;
-  int koff[2], voff[2];
+  int koff[CPT], voff[CPT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    const int c = tid + 512 * i;
+  for (int i = 0; i < CPT; ++i) {
+    const int c = tid + NT * i;
     koff[i] = (c >> 4) * krow_bytes + (c & 15) * 16;
     voff[i] = (c >> 4) * vrow_bytes + (c & 15) * 16;
   }
@@ -1450,15 +1461,15 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
   const uint16_t* vbase = p.v + kvh * p.v_sh + (PAGED ? 0 : b * p.v_sp);
   const int32_t* pt_row = PAGED ? p.page_table + static_cast<int64_t>(b) * p.max_pages : nullptr;
   struct Stage {
-    u32x4 k[2];
-    u32x4 v[2];
+    u32x4 k[CPT];
+    u32x4 v[CPT];
   };
   Stage st0, st1;
 
   // FUSED staging: per 32-key half, from the cache (keys before qs), from the new
   // rows (keys from qs on), or, for the half that holds qs, one load per lane from its
   // own row's source (rows past k_hi repeat row k_hi - 1, whose scores are masked).
-  const int hrow = tid >> 4;        // row of this thread's chunks within a 32-key half
+  const int hrow = tid >> 4;        // row of this thread's chunk 0 (chunk i: hrow + RPS i)
   const int hcol = (tid & 15) * 8;  // element column of the chunks
   const uint16_t* knbase = FUSED ? p.kn + b * p.n_sb + kvh * p.n_sh : nullptr;
   const uint16_t* vnbase = FUSED ? p.vn + b * p.n_sb + kvh * p.n_sh : nullptr;
@@ -1481,20 +1492,25 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
       return static_cast<int64_t>(key) * ss;
     }
   };
-  auto load_half_fused = [&](Stage& sg, int i, int kh) {
+  // the chunks of half `half` (32 keys from kh): chunk i holds key row hrow + RPS i of the tile
+  auto load_half_fused = [&](Stage& sg, int half, int kh) {
     const int valid = __builtin_amdgcn_readfirstlane(max(0, min(32, k_hi - kh)));
     const int qs = si.qs;
     const int page = half_page(kh);
     if (kh < qs && qs < kh + 32 && valid > 0) {  // wave-uniform
       // addresses of both sources, then one load per lane (same load count as below)
-      const int key = min(kh + hrow, k_hi - 1);
-      const uint16_t* kc = kbase + cache_off(page, key, true);
-      const uint16_t* vc = vbase + cache_off(page, key, false);
-      const uint16_t* kq = knbase + static_cast<int64_t>(key - qs) * p.n_ss;
-      const uint16_t* vq = vnbase + static_cast<int64_t>(key - qs) * p.n_ss;
-      const bool nw = key >= qs;
-      sg.k[i] = *reinterpret_cast<const u32x4*>((nw ? kq : kc) + hcol);
-      sg.v[i] = *reinterpret_cast<const u32x4*>((nw ? vq : vc) + hcol);
+#pragma unroll
+      for (int i = 0; i < CPT; ++i) {
+        if ((RPS * i) / 32 != half) continue;  // compile-time
+        const int key = min(kh + hrow + RPS * i - 32 * half, k_hi - 1);
+        const uint16_t* kc = kbase + cache_off(page, key, true);
+        const uint16_t* vc = vbase + cache_off(page, key, false);
+        const uint16_t* kq = knbase + static_cast<int64_t>(key - qs) * p.n_ss;
+        const uint16_t* vq = vnbase + static_cast<int64_t>(key - qs) * p.n_ss;
+        const bool nw = key >= qs;
+        sg.k[i] = *reinterpret_cast<const u32x4*>((nw ? kq : kc) + hcol);
+        sg.v[i] = *reinterpret_cast<const u32x4*>((nw ? vq : vc) + hcol);
+      }
       return;
     }
     const uint16_t* kp;
@@ -1514,12 +1530,17 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kp), 0, valid * kbytes, kBufferFlags);
     const __amdgpu_buffer_rsrc_t vr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vp), 0, valid * vbytes, kBufferFlags);
-    sg.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, hrow * kbytes + hcol * 2, 0, 0));
-    sg.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, hrow * vbytes + hcol * 2, 0, 0));
-  };
-  int noff[2];  // FUSED: byte offsets of this thread's chunks in a tile of new rows
 #pragma unroll
-  for (int i = 0; i < 2; ++i) noff[i] = (hrow + 32 * i) * nrow_bytes + hcol * 2;
+    for (int i = 0; i < CPT; ++i) {
+      if ((RPS * i) / 32 != half) continue;  // compile-time
+      const int row = hrow + RPS * i - 32 * half;
+      sg.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, row * kbytes + hcol * 2, 0, 0));
+      sg.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, row * vbytes + hcol * 2, 0, 0));
+    }
+  };
+  int noff[CPT];  // FUSED: byte offsets of this thread's chunks in a tile of new rows
+#pragma unroll
+  for (int i = 0; i < CPT; ++i) noff[i] = (hrow + RPS * i) * nrow_bytes + hcol * 2;
   auto load_tile = [&](Stage& sg, int j) {
     const int kb = k_lo + j * KT;
     if constexpr (FUSED) {
@@ -1532,7 +1553,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
         const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vnbase + noffs), 0,
                                                                             valid * nrow_bytes, kBufferFlags);
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < CPT; ++i) {
           sg.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, noff[i], 0, 0));
           sg.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, noff[i], 0, 0));
         }
@@ -1547,11 +1568,11 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
     }
     if constexpr (PAGED) {
       if (p.page_size < KT) {
-        // 32-key pages: chunk i of every thread lies in key half i of the tile
-        // (rows tid / 16 + 32 i), each half on its own page
+        // 32-key pages: chunk i of every thread (key row tid / 16 + RPS i) lies in key
+        // half (RPS i) / 32 of the tile, each half on its own page
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-          const int kh = kb + 32 * i;
+        for (int half = 0; half < 2; ++half) {
+          const int kh = kb + 32 * half;
           const int valid = __builtin_amdgcn_readfirstlane(max(0, min(32, k_hi - kh)));
           const int page = pt_row[min(kh >> p.page_shift, p.max_pages - 1)];
           const int slot0 = kh & (p.page_size - 1);
@@ -1561,10 +1582,14 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
                                                                               valid * krow_bytes, kBufferFlags);
           const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase + voffs), 0,
                                                                               valid * vrow_bytes, kBufferFlags);
-          sg.k[i] = __builtin_bit_cast(u32x4,
-                                       __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i] - 32 * i * krow_bytes, 0, 0));
-          sg.v[i] = __builtin_bit_cast(u32x4,
-                                       __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i] - 32 * i * vrow_bytes, 0, 0));
+#pragma unroll
+          for (int i = 0; i < CPT; ++i) {
+            if ((RPS * i) / 32 != half) continue;  // compile-time
+            sg.k[i] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i] - 32 * half * krow_bytes, 0, 0));
+            sg.v[i] = __builtin_bit_cast(
+                u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i] - 32 * half * vrow_bytes, 0, 0));
+          }
         }
         return;
       }
@@ -1586,7 +1611,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
     const __amdgpu_buffer_rsrc_t vr =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase + voffs), 0, valid * vrow_bytes, kBufferFlags);
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < CPT; ++i) {
       sg.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, 0));
       sg.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, 0));
     }
@@ -1595,8 +1620,8 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
     uint16_t* sk = sKV[buf];
     uint16_t* sv = sk + KBUF;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int c = tid + 512 * i;
+    for (int i = 0; i < CPT; ++i) {
+      const int c = tid + NT * i;
       *reinterpret_cast<u32x4*>(&sk[(c >> 4) * KS + (c & 15) * 8]) = sg.k[i];
       *reinterpret_cast<u32x4*>(&sv[((c >> 1) & 1) * VOFF + (c >> 4) * VS2 + ((c >> 2) & 3) * 16 + (c & 1) * 8]) =
           sg.v[i];
@@ -1693,28 +1718,62 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
     const int kb = k_lo + j * KT;
     if (j < ntiles && kb < lim_max) compute_tile(j & 1, kb);  // wave-uniform
   };
+  // FUSED: the owned new rows go into the cache before the loop, 2 NT 16-byte chunks of
+  // each tensor per round (two per thread). The first round's loads are issued with the
+  // first tiles' and wait alongside them; more rounds (> NT / 8 owned rows) run after.
+  const int own_n = FUSED ? max(0, w_hi - w_lo) * 16 : 0;  // chunks per tensor
+  struct Own {
+    u32x4 k[2], v[2];
+    int page[2];
+  };
+  auto own_load = [&](Own& o, int base) {
+    const int64_t roff = static_cast<int64_t>(w_lo - si.qs) * p.n_ss;
+    const __amdgpu_buffer_rsrc_t kr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(knbase + roff), 0, own_n > 0 ? (w_hi - w_lo) * nrow_bytes : 0, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(vnbase + roff), 0, own_n > 0 ? (w_hi - w_lo) * nrow_bytes : 0, kBufferFlags);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = base + tid + NT * i;  // row c / 16 of the owned range, chunk c % 16
+      const int off = (c >> 4) * nrow_bytes + (c & 15) * 16;
+      o.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
+      o.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0));
+      o.page[i] = 0;
+      if constexpr (PAGED) {
+        const int key = max(0, min(w_lo + (c >> 4), w_hi - 1));  // in range even with nothing owned
+        o.page[i] = pt_row[min(key >> p.page_shift, p.max_pages - 1)];
+      }
+    }
+  };
+  auto own_store = [&](const Own& o, int base) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = base + tid + NT * i;
+      if (c < own_n) {
+        const int key = w_lo + (c >> 4);
+        const int col = (c & 15) * 8;
+        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(kbase) + cache_off(o.page[i], key, true) + col) = o.k[i];
+        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(vbase) + cache_off(o.page[i], key, false) + col) = o.v[i];
+      }
+    }
+  };
+  Own own;
+  if constexpr (FUSED) own_load(own, 0);
   if (ntiles > 0) {
     load_tile(st0, 0);
     load_tile(st1, 1);
+  }
+  if constexpr (FUSED) {
+    own_store(own, 0);
+    for (int base = 2 * NT; base < own_n; base += 2 * NT) {
+      own_load(own, base);
+      own_store(own, base);
+    }
+  }
+  if (ntiles > 0) {
     for (int j = 0; j < ntiles; j += 2) {
       step(st0, j);
       step(st1, j + 1);
-    }
-  }
-  if constexpr (FUSED) {
-    // the owned new rows into the cache: the ones the loop staged were read last, so
-    // these reads are served by the L2; rows past the visible length were never staged
-    const int c_lo = w_lo;
-    for (int c = tid; c < (w_hi - c_lo) * 16; c += 512) {
-      const int key = c_lo + (c >> 4);
-      const int col = (c & 15) * 8;
-      const int64_t src = static_cast<int64_t>(key - si.qs) * p.n_ss + col;
-      int page = 0;
-      if constexpr (PAGED) page = pt_row[min(key >> p.page_shift, p.max_pages - 1)];
-      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(kbase) + cache_off(page, key, true) + col) =
-          *reinterpret_cast<const u32x4*>(knbase + src);
-      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(vbase) + cache_off(page, key, false) + col) =
-          *reinterpret_cast<const u32x4*>(vnbase + src);
     }
   }
 
@@ -1762,12 +1821,550 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_kernel(const AttnParams p) 
   }
 }
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer descriptor in scalar registers: base address, size in bytes, 32-bit format.
+__device__ __forceinline__ i32x4 make_srd(const void* base, int bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32));
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = kBufferFlags;
+  return r;
+}
+
+#ifndef FDLLM_PREFILL_PIPE
+#define FDLLM_PREFILL_PIPE 0
+#endif
+// Key halves (32 keys) whose page ids the ring prefill kernel stages in LDS: 65536 keys
+// per workgroup; longer paged ranges take kv_prefill_kernel.
+constexpr int kRingMaxHalves = 2048;
+
+// Direct-to-LDS load: 16 bytes per lane from buffer offset voff to LDS byte address
+// lds + 16 * lane (one 1 KB block per wave; lanes past the descriptor's size write
+// zeros without memory traffic). The compiler does not see the LDS write, so readers
+// wait with wait_vmcnt and a barrier; M0 is restored after the load.
+__device__ __forceinline__ void lds_dma16(i32x4 srd_in, int voff, uint32_t lds_in) {
+  // both are wave-uniform by construction; readfirstlane puts them in scalar registers
+  i32x4 srd;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) srd[i] = __builtin_amdgcn_readfirstlane(srd_in[i]);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_in);
+  int saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(srd), "s"(lds));
+}
+
+// Wait until at most N vector memory operations of this wave are outstanding.
+// Neither asm declares a memory clobber: such a clobber would keep every local whose
+// address a lambda captured in scratch memory. Their order against the LDS reads comes
+// from the workgroup barrier between them (volatile asm is not moved across the
+// barrier and its fences).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
+}
+
+// ---------------------------------------------------------------------------
+// Prefill attention with direct-to-LDS staging (same work split, math and results
+// as kv_prefill_kernel).
+//   * K / V tiles go from memory straight into a ring of four LDS slots
+//     (buffer_load ... lds), three tiles in flight, one barrier per tile; no
+//     staging registers and no LDS store instructions.
+//   * Wave w loads key rows [8 w, 8 w + 8) of each tile, 4 rows (1 KB) per load.
+//     Rows are 256 bytes without padding; bank conflicts of the MFMA operand reads
+//     are avoided by an XOR swizzle of the 16-byte chunks, applied on the source
+//     side: LDS chunk p of K row r holds column chunk p ^ (r & 15), of V row r
+//     chunk p ^ 4 (r & 3).
+template <bool F16, bool PAGED, bool SPLIT, bool FUSED>
+__global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParams p) {
+  constexpr int D = 128;
+  constexpr int KT = 64;
+  constexpr int NSLOT = 4;
+  constexpr int TB = KT * D * 2;       // bytes of one K (or V) tile
+  constexpr int VREG = NSLOT * TB;     // V slots follow the K slots
+  __shared__ __attribute__((aligned(1024))) uint8_t ring[2 * NSLOT * TB];
+  // page ids of the workgroup's 32-key halves, read once: a page-table load inside the
+  // loop would be a vector load the compiler waits for with vmcnt(0), which would also
+  // wait for every tile in flight
+  __shared__ int sPg[PAGED ? kRingMaxHalves : 1];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int n32 = lane & 31;
+  const int h = lane >> 5;
+  const int l16 = lane & 15;
+  const int g16 = lane >> 4;
+
+  int b, kvh, rb, k_lo, k_hi, n_act, split, first;
+  SeqInfo si;
+  if constexpr (SPLIT) {
+    kvh = blockIdx.y;
+    const DecodePart dp = decode_partition<PAGED, KT>(p);
+    if (dp.b < 0) return;  // idle slot (uniform over the workgroup)
+    b = __builtin_amdgcn_readfirstlane(dp.b);
+    split = __builtin_amdgcn_readfirstlane(dp.split);
+    n_act = __builtin_amdgcn_readfirstlane(dp.n_act);
+    first = __builtin_amdgcn_readfirstlane(dp.first);
+    k_lo = __builtin_amdgcn_readfirstlane(dp.k_lo);
+    k_hi = __builtin_amdgcn_readfirstlane(dp.k_hi);
+    rb = 0;
+    si.seqlen = dp.seqlen;
+    si.qs = dp.qs;
+    si.kv_end = dp.kv_end;
+  } else {
+    const int unit = blockIdx.x;
+    b = unit / p.Hkv;
+    kvh = unit - b * p.Hkv;
+    rb = p.n_rb - 1 - static_cast<int>(blockIdx.y);
+    si = seq_info<PAGED>(p, b, rb);
+    k_lo = 0;
+    k_hi = si.kv_end;
+    n_act = 1;
+    split = first = 0;
+  }
+  const int row0 = rb * 256;
+  const int ntiles = k_hi > k_lo ? (k_hi - k_lo + KT - 1) / KT : 0;
+  const int qs = si.qs;
+
+  // FUSED: new rows at key positions [w_lo, w_hi) are this workgroup's to store
+  int w_lo = 0, w_hi = 0;
+  if constexpr (FUSED) {
+    const int qend = qs + p.Sq;
+    if constexpr (SPLIT) {
+      w_lo = max(k_lo, qs);
+      w_hi = split == n_act - 1 ? qend : min(k_hi, qend);
+    } else {
+      w_lo = qs + (256 * rb) / p.G;
+      w_hi = qs + min(p.Sq, (256 * (rb + 1)) / p.G);
+    }
+    w_lo = __builtin_amdgcn_readfirstlane(max(w_lo, 0));
+    w_hi = __builtin_amdgcn_readfirstlane(min(w_hi, p.cap));
+  }
+
+  // ---- this lane's query row: Q^T fragments and key limit
+  const int r = row0 + wave * 32 + n32;
+  const int rc = min(r, p.R - 1);  // padding rows reuse a valid row: finite, never written
+  const int t = rc / p.G;
+  const int hh = rc - t * p.G;
+  const int lim = row_key_limit(p, si.seqlen, qs, t);
+  u32x4 qf[8];  // loaded after the first tiles are issued (see the main loop)
+  const int lim_min =
+      __builtin_amdgcn_readfirstlane(-static_cast<int>(wave_allreduce_max(-static_cast<float>(lim))));
+  const int lim_max = __builtin_amdgcn_readfirstlane(static_cast<int>(wave_allreduce_max(static_cast<float>(lim))));
+  const float c2 = p.scale_log2;
+  const float rescale_thr = 8.f / c2;
+
+  f32x16 acc[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) acc[dt][e] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;
+
+  const int krow_bytes = static_cast<int>(p.k_ss) * 2;
+  const int vrow_bytes = static_cast<int>(p.v_ss) * 2;
+  const uint16_t* kbase = p.k + kvh * p.k_sh + (PAGED ? 0 : b * p.k_sp);
+  const uint16_t* vbase = p.v + kvh * p.v_sh + (PAGED ? 0 : b * p.v_sp);
+  const int32_t* pt_row = PAGED ? p.page_table + static_cast<int64_t>(b) * p.max_pages : nullptr;
+  const uint16_t* knbase = FUSED ? p.kn + b * p.n_sb + kvh * p.n_sh : nullptr;
+  const uint16_t* vnbase = FUSED ? p.vn + b * p.n_sb + kvh * p.n_sh : nullptr;
+  const int nrow_bytes = FUSED ? static_cast<int>(p.n_ss) * 2 : 0;
+
+  // element offset of key's row from kbase / vbase, given the page of its 32-key half
+  auto cache_off = [&](int page, int key, bool kcache) __attribute__((always_inline)) -> int64_t {
+    const int64_t ss = kcache ? p.k_ss : p.v_ss;
+    if constexpr (PAGED) {
+      return static_cast<int64_t>(page) * (kcache ? p.k_sp : p.v_sp) + (key & (p.page_size - 1)) * ss;
+    } else {
+      return static_cast<int64_t>(key) * ss;
+    }
+  };
+  // page of the 32-key half starting at kh (pages of >= 32 keys hold whole halves)
+  const int n_halves = PAGED ? min(kRingMaxHalves, 2 * (ntiles + 6)) : 1;
+  auto half_page = [&](int kh) __attribute__((always_inline)) -> int {
+    if constexpr (PAGED) {
+      return sPg[min((kh - k_lo) >> 5, n_halves - 1)];
+    } else {
+      return 0;
+    }
+  };
+
+  // ---- DMA source offsets: load i (0, 1) of wave w covers tile rows 8 w + 4 i + lane / 16,
+  // lane % 16 = the chunk's place in the LDS row; all of a wave's rows lie in half w / 4
+  // (scalars, not arrays: a select between two arrays' elements would keep them in
+  // scratch memory)
+  const int half = __builtin_amdgcn_readfirstlane(wave >> 2);  // uniform: page lookups stay scalar loads
+  const int hrow0 = 8 * (wave & 3) + (lane >> 4);  // half row of load 0; load 1: + 4
+  const int hrow1 = hrow0 + 4;
+  const int kc0 = (lane & 15) ^ ((hrow0 + 32 * half) & 15), kc1 = (lane & 15) ^ ((hrow1 + 32 * half) & 15);
+  const int vc0 = (lane & 15) ^ ((hrow0 & 3) << 2), vc1 = (lane & 15) ^ ((hrow1 & 3) << 2);
+  const int kso0 = hrow0 * krow_bytes + (kc0 << 4), kso1 = hrow1 * krow_bytes + (kc1 << 4);
+  const int vso0 = hrow0 * vrow_bytes + (vc0 << 4), vso1 = hrow1 * vrow_bytes + (vc1 << 4);
+  const int knso0 = hrow0 * nrow_bytes + (kc0 << 4), knso1 = hrow1 * nrow_bytes + (kc1 << 4);
+  const int vnso0 = hrow0 * nrow_bytes + (vc0 << 4), vnso1 = hrow1 * nrow_bytes + (vc1 << 4);
+  const uint32_t ring_lds = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(ring));
+  const uint32_t kdst = ring_lds + 8 * wave * 256;
+  const uint32_t vdst = ring_lds + VREG + 8 * wave * 256;
+
+  // Tile tt into slot `slot`: 2 K and 2 V loads per wave (4 more where a 32-key half
+  // holds qs: each lane then loads from its own row's source under an exec mask).
+  auto issue = [&](int tt, int slot) __attribute__((always_inline)) {
+    const int kh = k_lo + tt * KT + 32 * half;
+    const int valid = __builtin_amdgcn_readfirstlane(max(0, min(32, k_hi - kh)));
+    const uint32_t kd = kdst + slot * TB;
+    const uint32_t vd = vdst + slot * TB;
+    const int page = half_page(kh);
+    if (FUSED && kh < qs && qs < kh + 32 && valid > 0) {
+      const i32x4 kc = make_srd(kbase + cache_off(page, kh, true), (qs - kh) * krow_bytes);
+      const i32x4 vc = make_srd(vbase + cache_off(page, kh, false), (qs - kh) * vrow_bytes);
+      const i32x4 kq = make_srd(knbase, (kh + valid - qs) * nrow_bytes);
+      const i32x4 vq = make_srd(vnbase, (kh + valid - qs) * nrow_bytes);
+      // per lane: row key - qs of the new rows, or row key - kh of the cache rows
+      const int d = (kh - qs) * nrow_bytes;  // shifts a new-row offset from half row hr to row kh + hr - qs
+      if (kh + hrow0 >= qs) {
+        lds_dma16(kq, knso0 + d, kd);
+        lds_dma16(vq, vnso0 + d, vd);
+      } else {
+        lds_dma16(kc, kso0, kd);
+        lds_dma16(vc, vso0, vd);
+      }
+      if (kh + hrow1 >= qs) {
+        lds_dma16(kq, knso1 + d, kd + 1024);
+        lds_dma16(vq, vnso1 + d, vd + 1024);
+      } else {
+        lds_dma16(kc, kso1, kd + 1024);
+        lds_dma16(vc, vso1, vd + 1024);
+      }
+      return;
+    }
+    i32x4 ks, vs;
+    const bool from_new = FUSED && kh >= qs;  // wave-uniform
+    if (from_new) {
+      const int64_t noffs = static_cast<int64_t>(kh - qs) * p.n_ss;
+      ks = make_srd(knbase + noffs, valid * nrow_bytes);
+      vs = make_srd(vnbase + noffs, valid * nrow_bytes);
+    } else {
+      ks = make_srd(kbase + cache_off(page, kh, true), valid * krow_bytes);
+      vs = make_srd(vbase + cache_off(page, kh, false), valid * vrow_bytes);
+    }
+    // value selects (a conditional of two named ints is an lvalue: clang would select
+    // their addresses and keep them in scratch memory)
+    const int sel = from_new ? 1 : 0;
+    lds_dma16(ks, kso0 + sel * (knso0 - kso0), kd);
+    lds_dma16(vs, vso0 + sel * (vnso0 - vso0), vd);
+    lds_dma16(ks, kso1 + sel * (knso1 - kso1), kd + 1024);
+    lds_dma16(vs, vso1 + sel * (vnso1 - vso1), vd + 1024);
+  };
+
+  // ---- MFMA operand addresses (bytes from ring): K row 32 st + n32, chunk 2 ks + h;
+  // V^T reads: rows 16 kk + 4 (g16 >> 1) + (l16 >> 2) (+ 8), columns 32 dt + 16 (g16 & 1) + 4 (l16 & 3)
+  int kaddr[8], vaddr[4];
+#pragma unroll
+  for (int ks = 0; ks < 8; ++ks) kaddr[ks] = n32 * 256 + (((2 * ks + h) ^ (n32 & 15)) << 4);
+  {
+    const int vrow = 4 * (g16 >> 1) + (l16 >> 2);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt) {
+      const int lc = 4 * dt + 2 * (g16 & 1) + ((l16 >> 1) & 1);
+      vaddr[dt] = VREG + vrow * 256 + ((lc ^ ((l16 >> 2) << 2)) << 4) + ((l16 & 1) << 3);
+    }
+  }
+
+  auto compute_tile = [&](int slot, int kb) __attribute__((always_inline)) {
+    const uint8_t* sk = ring + slot * TB;
+    const uint8_t* sv = ring + slot * TB;
+    f32x16 s[2];
+    {
+      u32x4 kf[8][2];
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) kf[ks][st] = *reinterpret_cast<const u32x4*>(sk + st * 8192 + kaddr[ks]);
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) s[st][e] = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) s[st] = mfma32x32x16<F16>(kf[ks][st], qf[ks], s[st]);
+      __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+#pragma unroll
+      for (int i = 0; i < 12; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    }
+    if (!(kb + KT <= lim_min)) {  // wave-uniform: some row of the wave sees part of the tile
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (kb + 32 * st + 8 * i + 4 * h + j >= lim) s[st][4 * i + j] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[st][e]);
+    mx = halves_max(mx);
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + rescale_thr) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = m_run == -INFINITY ? 0.f : fast_exp2((m_run - m_new) * c2);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = m_run == -INFINITY ? 0.f : m_run * c2;
+    float lsum = 0.f;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float v = fast_exp2(fmaf(s[st][e], c2, -mc));
+        s[st][e] = v;
+        lsum += v;
+      }
+    l_run += lsum;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int st = kk >> 1;
+      const int e0 = 8 * (kk & 1);
+      const u32x4 pf = {pack2<F16>(s[st][e0], s[st][e0 + 1]), pack2<F16>(s[st][e0 + 2], s[st][e0 + 3]),
+                        pack2<F16>(s[st][e0 + 4], s[st][e0 + 5]), pack2<F16>(s[st][e0 + 6], s[st][e0 + 7])};
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(reinterpret_cast<const uint16_t*>(
+                                                       sv + kk * 4096 + vaddr[dt])));
+        const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(reinterpret_cast<const uint16_t*>(
+                                                       sv + kk * 4096 + 2048 + vaddr[dt])));
+        acc[dt] = mfma32x32x16<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf, acc[dt]);
+      }
+    }
+  };
+
+  // ---- software-pipelined form (FDLLM_PREFILL_PIPE): the scores of tile j + 1 are
+  // computed while tile j's softmax runs, so that one wave's instruction stream
+  // alternates MFMA and VALU work instead of running them in turn.
+  // S = K Q^T of the tile in `slot` (the MFMAs are issued, not waited for)
+  auto qk = [&](int slot, f32x16 (&s)[2]) __attribute__((always_inline)) {
+    const uint8_t* sk = ring + slot * TB;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) s[st][e] = 0.f;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+        s[st] = mfma32x32x16<F16>(*reinterpret_cast<const u32x4*>(sk + st * 8192 + kaddr[ks]), qf[ks], s[st]);
+  };
+  auto mask = [&](f32x16 (&s)[2], int kb) __attribute__((always_inline)) {
+    if (!(kb + KT <= lim_min)) {  // wave-uniform: some row of the wave sees part of the tile
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            if (kb + 32 * st + 8 * i + 4 * h + j >= lim) s[st][4 * i + j] = -INFINITY;
+    }
+  };
+  // one step of the pipeline: sc = masked scores of tile j (slot), sn <- scores of tile
+  // j + 1 (slot1); then softmax and PV of tile j
+  auto pipe_step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], int slot, int slot1, int kb, bool active)
+                       __attribute__((always_inline)) {
+    qk(slot1, sn);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[st][e]);
+    mx = halves_max(mx);
+    // MFMA / DS read / VALU interleave of this region
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
+    }
+    if (!active) return;  // wave-uniform
+    if (__builtin_amdgcn_ballot_w64(mx > m_run + rescale_thr) != 0) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = m_run == -INFINITY ? 0.f : fast_exp2((m_run - m_new) * c2);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) acc[dt] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = m_run == -INFINITY ? 0.f : m_run * c2;
+    const uint8_t* sv = ring + slot * TB;
+    float lsum = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const int st = kk >> 1;
+      const int e0 = 8 * (kk & 1);
+#pragma unroll
+      for (int e = e0; e < e0 + 8; ++e) {
+        const float v = fast_exp2(fmaf(sc[st][e], c2, -mc));
+        sc[st][e] = v;
+        lsum += v;
+      }
+      const u32x4 pf = {pack2<F16>(sc[st][e0], sc[st][e0 + 1]), pack2<F16>(sc[st][e0 + 2], sc[st][e0 + 3]),
+                        pack2<F16>(sc[st][e0 + 4], sc[st][e0 + 5]), pack2<F16>(sc[st][e0 + 6], sc[st][e0 + 7])};
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(reinterpret_cast<const uint16_t*>(
+                                                       sv + kk * 4096 + vaddr[dt])));
+        const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(reinterpret_cast<const uint16_t*>(
+                                                       sv + kk * 4096 + 2048 + vaddr[dt])));
+        acc[dt] = mfma32x32x16<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf, acc[dt]);
+      }
+    }
+    l_run += lsum;
+  };
+
+  // ---- FUSED: the owned new rows into the cache, before any tile load is issued
+  if constexpr (FUSED) {
+    const int own_n = max(0, w_hi - w_lo) * 16;  // 16-byte chunks per tensor
+    const int64_t roff = static_cast<int64_t>(w_lo - qs) * p.n_ss;
+    for (int c = tid; c < own_n; c += 512) {
+      const int key = w_lo + (c >> 4);
+      const int col = (c & 15) * 8;
+      const int64_t src = roff + static_cast<int64_t>(c >> 4) * p.n_ss + col;
+      int page = 0;
+      if constexpr (PAGED) page = pt_row[min(key >> p.page_shift, p.max_pages - 1)];
+      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(kbase) + cache_off(page, key, true) + col) =
+          *reinterpret_cast<const u32x4*>(knbase + src);
+      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(vbase) + cache_off(page, key, false) + col) =
+          *reinterpret_cast<const u32x4*>(vnbase + src);
+    }
+  }
+
+  // ---- main loop: tile j in slot j % 4; tiles j + 1, j + 2 in flight; tile j + 3
+  // issued into the slot step j - 1 read, after the barrier that ends that step
+  auto step = [&](int j, int slot) __attribute__((always_inline)) {
+    wait_vmcnt<8>();  // this wave's loads of tile j have landed (two younger tiles in flight)
+    lds_barrier();    // ... and every wave's; every wave is done with step j - 1
+    issue(j + 3, (slot + 3) & 3);
+    const int kb = k_lo + j * KT;
+    if (j < ntiles && kb < lim_max) compute_tile(slot, kb);  // wave-uniform
+  };
+  if constexpr (PAGED) {
+    for (int i = tid; i < n_halves; i += 512) sPg[i] = pt_row[min((k_lo + 32 * i) >> p.page_shift, p.max_pages - 1)];
+    __syncthreads();
+  }
+  // The first three tiles, then the query fragments, then one wait for all of them.
+  // The compiler sees that wait (a builtin, unlike the loads' asm): it knows qf has
+  // landed and puts no wait of its own for qf inside the loop, where a vmcnt(0) would
+  // drain the tiles in flight every step.
+  if (ntiles > 0) {
+    issue(0, 0);
+    issue(1, 1);
+    issue(2, 2);
+  }
+  {
+    const uint16_t* qrow = p.q + b * p.q_sb + t * p.q_ss + (kvh * p.G + hh) * p.q_sh;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * h);
+  }
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15): vector memory only
+  if (ntiles > 0 && !FDLLM_PREFILL_PIPE) {
+    for (int j = 0; j < ntiles; j += 4) {
+      step(j, 0);
+      step(j + 1, 1);
+      step(j + 2, 2);
+      step(j + 3, 3);
+    }
+    wait_vmcnt<0>();  // no load may land in LDS after the workgroup ends
+  }
+  if (ntiles > 0 && FDLLM_PREFILL_PIPE) {
+    // tile j in slot j % 4 (V read at step j), tile j + 1 (K read at step j), tile j + 2
+    // in flight, tile j + 3 issued after the barrier
+    f32x16 sA[2], sB[2];
+    lds_barrier();  // tile 0 (waited for above) is in every wave's view
+    qk(0, sA);
+    mask(sA, k_lo);
+    auto pstep = [&](int j, int slot, f32x16 (&sc)[2], f32x16 (&sn)[2]) __attribute__((always_inline)) {
+      wait_vmcnt<4>();  // this wave's loads of tile j + 1 have landed (one younger tile in flight)
+      lds_barrier();    // ... and every wave's; every wave is done with step j - 1
+      issue(j + 3, (slot + 3) & 3);
+      const int kb = k_lo + j * KT;
+      pipe_step(sc, sn, slot, (slot + 1) & 3, kb, j < ntiles && kb < lim_max);
+      mask(sn, kb + KT);
+    };
+    for (int j = 0; j < ntiles; j += 4) {
+      pstep(j, 0, sA, sB);
+      pstep(j + 1, 1, sB, sA);
+      pstep(j + 2, 2, sA, sB);
+      pstep(j + 3, 3, sB, sA);
+    }
+    wait_vmcnt<0>();  // no load may land in LDS after the workgroup ends
+  }
+
+  // ---- epilogue: rows of both lane halves are whole after the exchange of l
+  l_run = halves_sum(l_run);
+  if constexpr (SPLIT) {
+    if (split == 0 && tid == 0 && p.ws_unit != nullptr) p.ws_unit[b * p.Hkv + kvh] = make_int2(first, n_act);
+  }
+  if (SPLIT && n_act > 1) {
+    const int64_t slot0 = first;
+    if (r < p.R) {
+      const int64_t slot = slot0 + split;
+      const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot * 256 * D, 0, 256 * D * 4, kBufferFlags);
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          __builtin_amdgcn_raw_buffer_store_b128(
+              __builtin_bit_cast(u32x4, f32x4{acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]}),
+              orsrc, (r * D + 32 * dt + 8 * i + 4 * h) * 4, 0, 0);
+      if (h == 0) {
+        const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot * 256, 0, 256 * 8, kBufferFlags);
+        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)), mrsrc, r * 8, 0,
+                                              0);
+      }
+    }
+    return;
+  }
+  if (r < p.R) {
+    const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+    uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int e = 4 * i;
+        *reinterpret_cast<u32x2*>(orow + 32 * dt + 8 * i + 4 * h) =
+            u32x2{pack2<F16>(acc[dt][e] * inv, acc[dt][e + 1] * inv),
+                  pack2<F16>(acc[dt][e + 2] * inv, acc[dt][e + 3] * inv)};
+      }
+  }
+}
+
 // Merge of the split prefill kernel's partials: grid (row chunks of 32, units),
 // 256 threads = 32 rows x 8 column groups. The unit's slots and split count come from
 // the table the kernel wrote in the same call; units with one split were written by
 // the kernel itself. Spreading the merge over the whole chip instead of the last
 // workgroup of each unit matters here: a unit's partials are 224 rows x 520 bytes
-// per split, several hundred KB, more than one compute unit reads quickly.
+// per split, several hundred KB, more than one compute unit reads quickly. Partial
+// rows stay fp32 in both split kernels. Measured and not kept, bf16 rows: the
+// full-block step went from 44.6 to 42.1 us on one box, but the 7B end-to-end greedy
+// agreement fell from 0.872 / 0.875 to 0.867 / 0.869 against a noise floor of 0.874
+// (s.e. 0.0013), a systematic loss; in the split decode kernel bf16 was also slower
+// (27.6 -> 27.9 us).
 template <bool F16>
 __global__ __launch_bounds__(256) void kv_split_prefill_merge_kernel(const AttnParams p) {
   const int unit = blockIdx.y;
@@ -2079,8 +2676,8 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
   if (prefill_shape) {
     pl->kind = kPlanPrefill;
     pl->MT = 4;
-    pl->rows_per_wg = 256;
-    pl->n_rb = (pl->R + 255) / 256;
+    pl->rows_per_wg = 32 * kPrefillWaves;
+    pl->n_rb = (pl->R + pl->rows_per_wg - 1) / pl->rows_per_wg;
     pl->n_splits = 1;
     pl->chunk = 1 << 30;
     pl->ws_o_bytes = pl->ws_ml_bytes = 0;
@@ -2130,15 +2727,35 @@ void launch_combine(const AttnParams& p, unsigned units, hipStream_t s) {
   kv_attn_combine_kernel<D, F16, PAGED><<<cgrid, dim3(256), 0, s>>>(p);
 }
 
+// The ring kernel (direct-to-LDS staging) takes prefill shapes; the split kernel for
+// full-block decode stays on register staging, which measured faster there (46.4 against
+// 47.3 us per full-block step: the ring kernel's first tiles and Q wait in series).
+#ifndef FDLLM_PREFILL_RING
+#define FDLLM_PREFILL_RING 1
+#endif
 template <bool SPLIT, bool FUSED>
 void launch_prefill(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
+  constexpr int NW = SPLIT ? 8 : kPrefillWaves;
   const bool paged = p.page_table != nullptr;
+  const dim3 block(64 * NW);
+  const int64_t max_keys = paged ? std::min<int64_t>(p.max_seqlen, static_cast<int64_t>(p.max_pages) * p.page_size)
+                                 : p.max_seqlen;
+  if (FDLLM_PREFILL_RING && !SPLIT && (!paged || max_keys + 6 * 64 <= static_cast<int64_t>(kRingMaxHalves) * 32)) {
+    if (f16) {
+      if (paged) kv_prefill_ring_kernel<true, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+      else kv_prefill_ring_kernel<true, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+    } else {
+      if (paged) kv_prefill_ring_kernel<false, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+      else kv_prefill_ring_kernel<false, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+    }
+    return;
+  }
   if (f16) {
-    if (paged) kv_prefill_kernel<true, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
-    else kv_prefill_kernel<true, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+    if (paged) kv_prefill_kernel<true, true, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(p);
+    else kv_prefill_kernel<true, false, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(p);
   } else {
-    if (paged) kv_prefill_kernel<false, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
-    else kv_prefill_kernel<false, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+    if (paged) kv_prefill_kernel<false, true, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(p);
+    else kv_prefill_kernel<false, false, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(p);
   }
 }
 

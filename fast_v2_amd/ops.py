@@ -17,6 +17,8 @@ in the manner of ``_wrap_flash_kvcache_as_custom_op``
                       Tensor? q_start, Tensor? page_table, int page_size) -> Tensor
     fdllm::gather_rmsnorm(Tensor hidden, Tensor indices, Tensor? weight, float eps,
                           int norm_mode, bool with_gathered) -> (Tensor, Tensor)
+    fdllm::kv_cache_write(Tensor k_new, Tensor v_new, Tensor(a!) k_cache, Tensor(b!) v_cache,
+                          Tensor? write_start, int write_offset, Tensor? positions) -> ()
 """
 from __future__ import annotations
 
@@ -514,6 +516,12 @@ _LIB.define(
 _LIB.define(
     "gather_rmsnorm(Tensor hidden, Tensor indices, Tensor? weight, float eps, "
     "int norm_mode, bool with_gathered) -> (Tensor, Tensor)")
+# the cache write mutates k_cache / v_cache in place: the (a!) / (b!) annotations let
+# torch.compile and functionalization see the mutation (the reference's compiled
+# forward writes with a traceable scatter_, static_kv_cache.py:218-229)
+_LIB.define(
+    "kv_cache_write(Tensor k_new, Tensor v_new, Tensor(a!) k_cache, Tensor(b!) v_cache, "
+    "Tensor? write_start, int write_offset, Tensor? positions) -> ()")
 
 
 def _flash_kvcache_impl(q, k_cache, v_cache, cache_seqlens, softmax_scale, causal):
@@ -553,6 +561,17 @@ def _gather_rmsnorm_meta(hidden, indices, weight, eps, norm_mode, with_gathered)
     return normed, gathered
 
 
+def _kv_cache_write_impl(k_new, v_new, k_cache, v_cache, write_start, write_offset, positions):
+    kv_cache_write(k_new, v_new, k_cache, v_cache, write_offset=write_offset, write_start=write_start,
+                   positions=positions)
+
+
+def _kv_cache_write_meta(k_new, v_new, k_cache, v_cache, write_start, write_offset, positions):
+    return None
+
+
+_LIB.impl("kv_cache_write", _kv_cache_write_impl, "CUDA")
+_LIB.impl("kv_cache_write", _kv_cache_write_meta, "Meta")
 _LIB.impl("flash_kvcache", _flash_kvcache_impl, "CUDA")
 _LIB.impl("flash_kvcache", _flash_kvcache_meta, "Meta")
 _LIB.impl("block_attn", _block_attn_impl, "CUDA")

@@ -137,10 +137,13 @@ class StaticKVCache:
         self._write_start.copy_(self.kv_write_start.to(torch.int32).expand(self.batch_size))
 
     def write_scratch_compiled(self, key_states, value_states, layer_idx) -> None:
-        """Write at ``kv_write_start`` without advancing the pointer (:218-229)."""
+        """Write at ``kv_write_start`` without advancing the pointer (:218-229).
+
+        Goes through the ``fdllm::kv_cache_write`` op (in-place mutation of the layer's
+        buffers declared in its schema), so torch.compile traces it without a break."""
         self._check_states(key_states, value_states)
-        ops.kv_cache_write(key_states, value_states, self.key_cache[layer_idx], self.value_cache[layer_idx],
-                           write_start=self._write_start)
+        torch.ops.fdllm.kv_cache_write(key_states, value_states, self.key_cache[layer_idx],
+                                       self.value_cache[layer_idx], self._write_start, 0, None)
 
     def write_sparse(self, key_states, value_states, layer_idx, write_positions) -> None:
         """Write token t of sequence b at position ``write_positions[b, t]`` (:231-247)."""

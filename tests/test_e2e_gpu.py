@@ -17,7 +17,7 @@ free-running (two independent generations; one flipped near-tie changes everythi
 after it in the block, so this rate is low with random weights and is reported only).
 At 28 layers of random weights, ulp-level differences in summation order already flip
 about a tenth of the near-tied greedy choices, so the HIP run is held to the agreement
-of the two oracles with each other (the noise floor of the metric) minus 0.03.
+of the two oracles with each other (the noise floor of the metric).
 """
 import pytest
 import torch
@@ -173,26 +173,121 @@ def test_generation_agreement_small(gpu, use_block_cache):
     assert forced_bf16p > 0.95 and forced_f32 > 0.9
 
 
-def test_generation_7b_bs16(gpu):
-    """The end-to-end geometry: 28 layers, batch 16, 512-token prompts, 32-token blocks with
-    8-token sub-blocks, threshold 0.9, block cache on; 256 new tokens (8 blocks) keep the
-    three generations of this test short."""
+@pytest.mark.timeout(900)
+def test_generation_7b_bs16(gpu, capsys):
+    """The end-to-end workload at full length: 28 layers, batch 16, 512-token prompts,
+    1024 new tokens in 32-token blocks with 8-token sub-blocks, threshold 0.9, block cache
+    on. Reports (to the terminal, uncaptured) the teacher-forced greedy agreement of the
+    HIP run with the bf16-P oracle and with the fp32 oracle, and the noise floor of the
+    metric: the two oracles (which differ only in where the probabilities are rounded)
+    against each other.
+
+    Bar: agreement with each oracle at least the floor minus three binomial standard
+    errors of a rate over this many positions (about 0.4 points at 70k positions), so a
+    systematic error that moves the HIP run further from the oracles than the oracles are
+    from each other by more than that fails. (Measured on MI355X: 0.8721 against the
+    bf16-P oracle, 0.8751 against the fp32 oracle, floor 0.8739, s.e. 0.0013.)"""
     cfg = em.BlockDiffusionConfig()
     model = em.build_model(cfg, gpu)
-    B, P, N = 16, 512, 256
+    B, P, N = 16, 512, 1024
     x = _prompts(B, P, cfg.vocab_size, seed=0).to(gpu)
-    print("7B bs16: HIP generation", flush=True)
+
+    def say(msg):
+        with capsys.disabled():
+            print(f"\n[e2e 7B bs16] {msg}", flush=True)
+    say(f"HIP generation of {N} tokens")
     rec, hip, st_h = _record(model, x, N, True)
-    print("7B bs16: oracle generations (teacher-forced)", flush=True)
-    forced_bf16p = _forced_rate(model, x, N, True, rec, hip, EagerStaticAttention(p_bf16=True))
+    say(f"HIP: {st_h.tokens_per_second:.1f} tok/s ({st_h.forwards} forwards, {st_h.seconds:.2f} s); "
+        "teacher-forced bf16-P oracle")
+    rep = _Replay(rec)
+    forced, _ = es.generate(model, x, max_new_tokens=N, use_block_cache=True, impl=EagerStaticAttention(p_bf16=True),
+                            policy=rep, bridge_policy=rep.bridge)
+    assert torch.equal(forced, hip)
+    forced_bf16p, n_pos = rep.rate, rep.total
+    say(f"agreement with the bf16-P oracle {forced_bf16p:.4f} over {n_pos} positions; teacher-forced fp32 oracle")
     forced_f32 = _forced_rate(model, x, N, True, rec, hip, EagerStaticAttention())
-    # noise floor of the metric at this depth: the two oracles (which differ only in where
-    # the probabilities are rounded) against each other
-    print("7B bs16: oracle-vs-oracle noise floor", flush=True)
+    say(f"agreement with the fp32 oracle {forced_f32:.4f}; oracle-vs-oracle floor")
     rec_o, traj_o, _ = _record(model, x, N, True, impl=EagerStaticAttention())
     floor = _forced_rate(model, x, N, True, rec_o, traj_o, EagerStaticAttention(p_bf16=True))
-    print(f"7B bs16: teacher-forced greedy agreement {forced_bf16p:.4f} (bf16-P oracle), {forced_f32:.4f} "
-          f"(fp32 oracle); oracle vs oracle {floor:.4f}; hip {st_h.tokens_per_second:.1f} tok/s "
-          f"({st_h.forwards} forwards, {st_h.seconds:.2f} s)")
+    se = (floor * (1.0 - floor) / max(n_pos, 1)) ** 0.5
+    say(f"teacher-forced greedy agreement over {N} tokens x {B} sequences: HIP vs bf16-P oracle "
+        f"{forced_bf16p:.4f}, HIP vs fp32 oracle {forced_f32:.4f}, fp32 oracle vs bf16-P oracle (floor) "
+        f"{floor:.4f} (binomial s.e. {se:.4f})")
     assert st_h.generated_tokens == B * N
-    assert min(forced_bf16p, forced_f32) > floor - 0.03
+    assert forced_bf16p >= floor - 3 * se
+    assert forced_f32 >= floor - 3 * se
+
+
+def test_compiled_forward_surface(gpu):
+    """patch_attention_layers_compiled (utils/attention_backends.py:901-974, :995-1012):
+    the branch-free diffusion-step forward. The prompt is committed with the patched
+    forward, then one 32-token diffusion step runs through the compiled forward; its
+    logits and the cache rows it wrote match the eager oracle doing the same, and
+    torch.compile's tracer (dynamo) takes one layer's compiled forward, cache write and
+    attention included, as a single graph without a break."""
+    from fast_v2_amd.utils import StaticKVCache
+    from fast_v2_amd.utils import attention_backends as ab
+    from oracle.e2e_eager import TorchKVCache
+
+    cfg = _small_cfg()
+    model = em.build_model(cfg, gpu)
+    B, P, S = 4, 64, 32
+    x = _prompts(B, P + S, cfg.vocab_size, seed=4).to(gpu)
+    pos = torch.arange(P, P + S, device=gpu)
+    backend = ab.get_attention_backend("hip")
+    L, Hkv, D = cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim
+
+    cache = StaticKVCache(B, 256, L, Hkv, D, torch.bfloat16, gpu)
+    orig = ab.patch_attention_layers(model, backend)
+    try:
+        model(x[:, :P], cache, update_past_key_values=True)
+    finally:
+        ab.unpatch_attention_layers(model, orig)
+    cache.set_kv_write_start(P)
+    cache.set_scratch_seqlens(P + S)
+    cache.prepare_write_idx(S)
+    orig = ab.patch_attention_layers_compiled(model, backend)
+    try:
+        got = model(x[:, P:P + S], cache, cache_position=pos, logits_to_keep=S).float()
+        # the rows written so far (the dynamo run below writes its own into layer 1)
+        written = [tuple(t[:, :P + S].clone() for t in cache.get_full_kv(layer)) for layer in range(L)]
+        # dynamo on one layer's compiled forward: no graph break (custom ops for the
+        # cache write and the attention, both with Meta implementations)
+        attn = model.model.layers[1].self_attn
+        h = torch.randn(B, S, cfg.hidden_size, generator=torch.Generator().manual_seed(5)).to(torch.bfloat16).to(gpu)
+        pe = model.model.rotary(pos, torch.bfloat16)
+        torch._dynamo.reset()
+        expl = torch._dynamo.explain(attn.forward)(h, pe, None, cache, pos)
+        print(f"compiled forward: {expl.graph_count} graph(s), {expl.graph_break_count} break(s), "
+              f"ops {expl.op_count}", flush=True)
+        assert expl.graph_break_count == 0, expl.break_reasons
+        assert expl.graph_count == 1
+    finally:
+        ab.unpatch_attention_layers(model, orig)
+        torch._dynamo.reset()
+
+    ref_impl = EagerStaticAttention()
+    rcache = TorchKVCache(B, 256, L, Hkv, D, torch.bfloat16, gpu)
+    orig = ref_impl.patch(model, None)
+    try:
+        model(x[:, :P], rcache, update_past_key_values=True)
+        rcache.set_kv_write_start(P)
+        rcache.set_scratch_seqlens(P + S)
+        exp = model(x[:, P:P + S], rcache, cache_position=pos, logits_to_keep=S).float()
+    finally:
+        ref_impl.unpatch(model, orig)
+    rel = ((got - exp).norm() / exp.norm()).item()
+    print(f"compiled forward: relative logit error {rel:.2e}", flush=True)
+    assert rel < 2e-2
+    for layer in range(L):
+        # committed prompt rows and the step's rows (written at kv_write_start). Layer 0's
+        # rows come from the same embeddings and projections on both paths; deeper layers'
+        # inputs carry the bf16-level differences of the attention outputs before them, so
+        # those are held to a relative-norm bound like the logits
+        k_hip, v_hip = written[layer]
+        k_ref, v_ref = rcache.get_full_kv(layer)
+        for a, b in ((k_hip, k_ref[:, :P + S]), (v_hip, v_ref[:, :P + S])):
+            a, b = a.float(), b.float()
+            if layer == 0:
+                torch.testing.assert_close(a, b, atol=2e-2, rtol=2e-2)
+            assert ((a - b).norm() / b.norm()).item() < 1e-2
