@@ -372,7 +372,7 @@ def bench_e2e(torch, args):
            "tokens_per_step": round(sum(st.step_tokens) / max(len(st.step_tokens), 1), 3),
            "params": em.param_count(cfg), "model_build_s": round(build_s, 2),
            "gemm_tuning": "torch TunableOp over hipBLASLt / rocBLAS solutions, tuned in the warm-up",
-           "forwards_graphed": "diffusion steps replayed from HIP graphs; commits eager",
+           "forwards_graphed": "prompt prefill, diffusion steps and commits replayed from HIP graphs",
            "weights": args.e2e_weights or ("random init (N(0, 0.02), zero biases, unit norms) except the mask "
                                            "token's lm_head row, which is zero: a random model may otherwise "
                                            "predict the mask token, which the unmask rule writes back, and the "

@@ -34,6 +34,12 @@ HIPCC_FLAGS = [
     "-mcode-object-version=5",
     # Packed fp32 ops stay off: hipcc would otherwise form v_pk_{add,mul,fma}_f32.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Kernel-argument preloading: a kernel's leading scalar and pointer arguments (not
+    # by-value structs) arrive in SGPRs at wave launch instead of by a load from the
+    # argument segment, which takes one memory round trip off the front of the kernels
+    # that lead with the pointers their first loads need (the gather went from 4.78 to
+    # 4.40 us). Code objects keep the compatibility prologue that loads them the old way.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
     "-Wno-unused-command-line-argument",
 ]
 

@@ -56,6 +56,9 @@ constexpr int kMaxDecodeSplits = 16;  // key splits per (sequence, KV head) in t
 #define FDLLM_DECODE_STAGES 2
 #endif
 constexpr int kDecodeStages = FDLLM_DECODE_STAGES;  // tiles in flight per workgroup in the split decode kernel
+#ifndef FDLLM_XCD_SLOTS
+#define FDLLM_XCD_SLOTS 0
+#endif
 // Waves (x 32 query rows) per prefill workgroup. Measured and not kept: 4 waves (two
 // independent workgroups per CU, so that their softmax and MFMA phases drift apart):
 // 549 us against 516-523 us for the 4 x 4096 prefill, the doubled K/V staging per
@@ -845,7 +848,16 @@ __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
   const int n_l = has ? active_splits(t, n_split) : 0;
   const int size_l = t > 0 ? ceil_div_small(t, n_split) : 0;
   const int incl = wave_incl_scan_i32(n_l);
+#if FDLLM_XCD_SLOTS
+  // slots in XCD-major order: workgroups are dealt to the 8 XCDs round-robin by linear
+  // id (x + S y here), so with S a multiple of 8 the workgroups of XCD j take slots
+  // j S / 8 .. (j + 1) S / 8 - 1, and the consecutive splits of one sequence share an
+  // L2 (their query rows are fetched from memory once)
+  const int slot = (S & 7) == 0 ? static_cast<int>(blockIdx.x & 7) * (S >> 3) + static_cast<int>(blockIdx.x >> 3)
+                                : static_cast<int>(blockIdx.x);
+#else
   const int slot = blockIdx.x;
+#endif
   const uint64_t mine = __builtin_amdgcn_ballot_w64(has && incl > slot);
   if (mine == 0) {
     dp.b = -1;
@@ -1346,7 +1358,8 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, c
 //     copy's loads are issued with the first tiles' and share their wait. Measured and
 //     not kept: stores from the staging registers inside the loop (the address
 //     arithmetic and branches sat in every step), and the copy after the loop (its
-//     load latency then sat at the end of every workgroup).
+//     load latency then sat at the end of every workgroup; its stores alone there
+//     were slower too).
 template <bool F16, bool PAGED, bool SPLIT, bool FUSED, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void kv_prefill_kernel(const AttnParams p) {
   constexpr int D = 128;
@@ -1834,8 +1847,11 @@ __device__ __forceinline__ i32x4 make_srd(const void* base, int bytes) {
   return r;
 }
 
+// 1: the ping-pong schedule below (two tiles in flight); 0: the plain schedule (three
+// tiles in flight, every wave runs S, softmax, PV in turn). On the 4 x 4096-token
+// prefill the ping-pong form measured 475-482 us against 484-488 us for the plain one.
 #ifndef FDLLM_PREFILL_PIPE
-#define FDLLM_PREFILL_PIPE 0
+#define FDLLM_PREFILL_PIPE 1
 #endif
 // Key halves (32 keys) whose page ids the ring prefill kernel stages in LDS: 65536 keys
 // per workgroup; longer paged ranges take kv_prefill_kernel.
@@ -2016,12 +2032,33 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParam
 
   // Tile tt into slot `slot`: 2 K and 2 V loads per wave (4 more where a 32-key half
   // holds qs: each lane then loads from its own row's source under an exec mask).
-  auto issue = [&](int tt, int slot) __attribute__((always_inline)) {
+  // mode (a constant at every call site, so each loop copy below folds it away):
+  // 0 every key from the cache, 1 every key from the new rows, 2 either, per half / lane
+  auto issue = [&](int tt, int slot, const int mode) __attribute__((always_inline)) {
     const int kh = k_lo + tt * KT + 32 * half;
     const int valid = __builtin_amdgcn_readfirstlane(max(0, min(32, k_hi - kh)));
     const uint32_t kd = kdst + slot * TB;
     const uint32_t vd = vdst + slot * TB;
+    if (mode == 1) {
+      const int64_t noffs = static_cast<int64_t>(kh - qs) * p.n_ss;
+      const i32x4 ks = make_srd(knbase + noffs, valid * nrow_bytes);
+      const i32x4 vs = make_srd(vnbase + noffs, valid * nrow_bytes);
+      lds_dma16(ks, knso0, kd);
+      lds_dma16(vs, vnso0, vd);
+      lds_dma16(ks, knso1, kd + 1024);
+      lds_dma16(vs, vnso1, vd + 1024);
+      return;
+    }
     const int page = half_page(kh);
+    if (mode == 0) {
+      const i32x4 ks = make_srd(kbase + cache_off(page, kh, true), valid * krow_bytes);
+      const i32x4 vs = make_srd(vbase + cache_off(page, kh, false), valid * vrow_bytes);
+      lds_dma16(ks, kso0, kd);
+      lds_dma16(vs, vso0, vd);
+      lds_dma16(ks, kso1, kd + 1024);
+      lds_dma16(vs, vso1, vd + 1024);
+      return;
+    }
     if (FUSED && kh < qs && qs < kh + 32 && valid > 0) {
       const i32x4 kc = make_srd(kbase + cache_off(page, kh, true), (qs - kh) * krow_bytes);
       const i32x4 vc = make_srd(vbase + cache_off(page, kh, false), (qs - kh) * vrow_bytes);
@@ -2155,12 +2192,18 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParam
     }
   };
 
-  // ---- software-pipelined form (FDLLM_PREFILL_PIPE): the scores of tile j + 1 are
-  // computed while tile j's softmax runs, so that one wave's instruction stream
-  // alternates MFMA and VALU work instead of running them in turn.
-  // S = K Q^T of the tile in `slot` (the MFMAs are issued, not waited for)
+  // ---- ping-pong form (FDLLM_PREFILL_PIPE): each wave alternates an MFMA phase (PV of
+  // tile j - 1, then S of tile j) and a VALU phase (softmax of tile j into packed P), and
+  // the two waves of a SIMD (w and w + 4) run half a step apart: waves 0-3 pass the
+  // step's barrier before their MFMA phase, waves 4-7 before their VALU phase, so on
+  // every SIMD one wave's MFMAs run beside the other wave's softmax.
   auto qk = [&](int slot, f32x16 (&s)[2]) __attribute__((always_inline)) {
     const uint8_t* sk = ring + slot * TB;
+    u32x4 kf[8][2];
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+#pragma unroll
+      for (int st = 0; st < 2; ++st) kf[ks][st] = *reinterpret_cast<const u32x4*>(sk + st * 8192 + kaddr[ks]);
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
@@ -2168,10 +2211,31 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParam
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
-      for (int st = 0; st < 2; ++st)
-        s[st] = mfma32x32x16<F16>(*reinterpret_cast<const u32x4*>(sk + st * 8192 + kaddr[ks]), qf[ks], s[st]);
+      for (int st = 0; st < 2; ++st) s[st] = mfma32x32x16<F16>(kf[ks][st], qf[ks], s[st]);
+    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+#pragma unroll
+    for (int i = 0; i < 12; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
   };
-  auto mask = [&](f32x16 (&s)[2], int kb) __attribute__((always_inline)) {
+  auto pv = [&](const u32x4 (&P)[4], int slot) __attribute__((always_inline)) {
+    const uint8_t* sv = ring + slot * TB;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(reinterpret_cast<const uint16_t*>(
+                                                       sv + kk * 4096 + vaddr[dt])));
+        const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(reinterpret_cast<const uint16_t*>(
+                                                       sv + kk * 4096 + 2048 + vaddr[dt])));
+        acc[dt] = mfma32x32x16<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, P[kk], acc[dt]);
+      }
+  };
+  // softmax of the scores s of the tile at keys kb: mask, running max (lazy rescale of
+  // acc), exponentials, running sum; P = the probabilities packed as the PV operand
+  auto softmax_p = [&](f32x16 (&s)[2], int kb, u32x4 (&P)[4]) __attribute__((always_inline)) {
     if (!(kb + KT <= lim_min)) {  // wave-uniform: some row of the wave sees part of the tile
 #pragma unroll
       for (int st = 0; st < 2; ++st)
@@ -2181,26 +2245,12 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParam
           for (int j = 0; j < 4; ++j)
             if (kb + 32 * st + 8 * i + 4 * h + j >= lim) s[st][4 * i + j] = -INFINITY;
     }
-  };
-  // one step of the pipeline: sc = masked scores of tile j (slot), sn <- scores of tile
-  // j + 1 (slot1); then softmax and PV of tile j
-  auto pipe_step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], int slot, int slot1, int kb, bool active)
-                       __attribute__((always_inline)) {
-    qk(slot1, sn);
     float mx = -INFINITY;
 #pragma unroll
     for (int st = 0; st < 2; ++st)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, sc[st][e]);
+      for (int e = 0; e < 16; ++e) mx = fmaxf(mx, s[st][e]);
     mx = halves_max(mx);
-    // MFMA / DS read / VALU interleave of this region
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);  // VALU
-    }
-    if (!active) return;  // wave-uniform
     if (__builtin_amdgcn_ballot_w64(mx > m_run + rescale_thr) != 0) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = m_run == -INFINITY ? 0.f : fast_exp2((m_run - m_new) * c2);
@@ -2210,55 +2260,72 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParam
       m_run = m_new;
     }
     const float mc = m_run == -INFINITY ? 0.f : m_run * c2;
-    const uint8_t* sv = ring + slot * TB;
     float lsum = 0.f;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float v = fast_exp2(fmaf(s[st][e], c2, -mc));
+        s[st][e] = v;
+        lsum += v;
+      }
+    l_run += lsum;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int st = kk >> 1;
       const int e0 = 8 * (kk & 1);
-#pragma unroll
-      for (int e = e0; e < e0 + 8; ++e) {
-        const float v = fast_exp2(fmaf(sc[st][e], c2, -mc));
-        sc[st][e] = v;
-        lsum += v;
-      }
-      const u32x4 pf = {pack2<F16>(sc[st][e0], sc[st][e0 + 1]), pack2<F16>(sc[st][e0 + 2], sc[st][e0 + 3]),
-                        pack2<F16>(sc[st][e0 + 4], sc[st][e0 + 5]), pack2<F16>(sc[st][e0 + 6], sc[st][e0 + 7])};
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt) {
-        const u32x2 lo = __builtin_bit_cast(u32x2, lds_read_tr16(reinterpret_cast<const uint16_t*>(
-                                                       sv + kk * 4096 + vaddr[dt])));
-        const u32x2 hi = __builtin_bit_cast(u32x2, lds_read_tr16(reinterpret_cast<const uint16_t*>(
-                                                       sv + kk * 4096 + 2048 + vaddr[dt])));
-        acc[dt] = mfma32x32x16<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, pf, acc[dt]);
-      }
+      P[kk] = u32x4{pack2<F16>(s[st][e0], s[st][e0 + 1]), pack2<F16>(s[st][e0 + 2], s[st][e0 + 3]),
+                    pack2<F16>(s[st][e0 + 4], s[st][e0 + 5]), pack2<F16>(s[st][e0 + 6], s[st][e0 + 7])};
     }
-    l_run += lsum;
   };
 
-  // ---- FUSED: the owned new rows into the cache, before any tile load is issued
-  if constexpr (FUSED) {
-    const int own_n = max(0, w_hi - w_lo) * 16;  // 16-byte chunks per tensor
+  // ---- FUSED: the owned new rows into the cache. The first 1024 chunks of each tensor
+  // (64 rows; all of them at GQA >= 4) are loaded before the first tiles are issued and
+  // stored after the common wait below, so their round trip overlaps the tiles' and
+  // Q's; any further rows are copied after that, in rounds. Measured and not kept: the
+  // stores after the loop (498 us against 486-492 us on the 4 x 4096 prefill).
+  const int own_n = FUSED ? max(0, w_hi - w_lo) * 16 : 0;  // 16-byte chunks per tensor
+  u32x4 own_k[2], own_v[2];
+  int own_pg[2] = {0, 0};
+  auto own_load = [&](int base) __attribute__((always_inline)) {
     const int64_t roff = static_cast<int64_t>(w_lo - qs) * p.n_ss;
-    for (int c = tid; c < own_n; c += 512) {
-      const int key = w_lo + (c >> 4);
-      const int col = (c & 15) * 8;
-      const int64_t src = roff + static_cast<int64_t>(c >> 4) * p.n_ss + col;
-      int page = 0;
-      if constexpr (PAGED) page = pt_row[min(key >> p.page_shift, p.max_pages - 1)];
-      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(kbase) + cache_off(page, key, true) + col) =
-          *reinterpret_cast<const u32x4*>(knbase + src);
-      *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(vbase) + cache_off(page, key, false) + col) =
-          *reinterpret_cast<const u32x4*>(vnbase + src);
+    const int bytes = own_n > 0 ? (w_hi - w_lo) * nrow_bytes : 0;
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(knbase + roff), 0, bytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vnbase + roff), 0, bytes, kBufferFlags);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = base + tid + 512 * i;  // row c / 16 of the owned range, chunk c % 16
+      const int off = (c >> 4) * nrow_bytes + (c & 15) * 16;
+      own_k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, off, 0, 0));
+      own_v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, off, 0, 0));
+      if constexpr (PAGED) {
+        const int key = max(0, min(w_lo + (c >> 4), w_hi - 1));  // in range even with nothing owned
+        own_pg[i] = pt_row[min(key >> p.page_shift, p.max_pages - 1)];
+      }
     }
-  }
+  };
+  auto own_store = [&](int base) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = base + tid + 512 * i;
+      if (c < own_n) {
+        const int key = w_lo + (c >> 4);
+        const int col = (c & 15) * 8;
+        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(kbase) + cache_off(own_pg[i], key, true) + col) = own_k[i];
+        *reinterpret_cast<u32x4*>(const_cast<uint16_t*>(vbase) + cache_off(own_pg[i], key, false) + col) = own_v[i];
+      }
+    }
+  };
+  if constexpr (FUSED) own_load(0);
 
   // ---- main loop: tile j in slot j % 4; tiles j + 1, j + 2 in flight; tile j + 3
   // issued into the slot step j - 1 read, after the barrier that ends that step
-  auto step = [&](int j, int slot) __attribute__((always_inline)) {
+  auto step = [&](int j, int slot, const int mode) __attribute__((always_inline)) {
     wait_vmcnt<8>();  // this wave's loads of tile j have landed (two younger tiles in flight)
     lds_barrier();    // ... and every wave's; every wave is done with step j - 1
-    issue(j + 3, (slot + 3) & 3);
+    issue(j + 3, (slot + 3) & 3, mode);
     const int kb = k_lo + j * KT;
     if (j < ntiles && kb < lim_max) compute_tile(slot, kb);  // wave-uniform
   };
@@ -2270,10 +2337,24 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParam
   // The compiler sees that wait (a builtin, unlike the loads' asm): it knows qf has
   // landed and puts no wait of its own for qf inside the loop, where a vmcnt(0) would
   // drain the tiles in flight every step.
+  // source of the keys: the cache only (no new rows, or all of them past k_hi), the new
+  // rows only (the plain prefill: qs <= k_lo), or both
+  const int src_mode = !FUSED || qs >= k_hi ? 0 : (qs <= k_lo ? 1 : 2);
+  // tiles 0, 1 (and 2 for the plain form, which keeps three in flight)
   if (ntiles > 0) {
-    issue(0, 0);
-    issue(1, 1);
-    issue(2, 2);
+    if (src_mode == 0) {
+      issue(0, 0, 0);
+      issue(1, 1, 0);
+      if (!FDLLM_PREFILL_PIPE) issue(2, 2, 0);
+    } else if (src_mode == 1) {
+      issue(0, 0, 1);
+      issue(1, 1, 1);
+      if (!FDLLM_PREFILL_PIPE) issue(2, 2, 1);
+    } else {
+      issue(0, 0, 2);
+      issue(1, 1, 2);
+      if (!FDLLM_PREFILL_PIPE) issue(2, 2, 2);
+    }
   }
   {
     const uint16_t* qrow = p.q + b * p.q_sb + t * p.q_ss + (kvh * p.G + hh) * p.q_sh;
@@ -2281,36 +2362,73 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParam
     for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * h);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15): vector memory only
-  if (ntiles > 0 && !FDLLM_PREFILL_PIPE) {
-    for (int j = 0; j < ntiles; j += 4) {
-      step(j, 0);
-      step(j + 1, 1);
-      step(j + 2, 2);
-      step(j + 3, 3);
+  if constexpr (FUSED) {
+    own_store(0);
+    for (int base = 1024; base < own_n; base += 1024) {  // more than 64 owned rows (GQA < 4)
+      own_load(base);
+      own_store(base);
     }
+  }
+  auto run = [&](const int mode) __attribute__((always_inline)) {
+    for (int j = 0; j < ntiles; j += 4) {
+      step(j, 0, mode);
+      step(j + 1, 1, mode);
+      step(j + 2, 2, mode);
+      step(j + 3, 3, mode);
+    }
+  };
+  if (ntiles > 0 && !FDLLM_PREFILL_PIPE) {
+    if (src_mode == 0) run(0);
+    else if (src_mode == 1) run(1);
+    else run(2);
     wait_vmcnt<0>();  // no load may land in LDS after the workgroup ends
   }
   if (ntiles > 0 && FDLLM_PREFILL_PIPE) {
-    // tile j in slot j % 4 (V read at step j), tile j + 1 (K read at step j), tile j + 2
-    // in flight, tile j + 3 issued after the barrier
-    f32x16 sA[2], sB[2];
-    lds_barrier();  // tile 0 (waited for above) is in every wave's view
-    qk(0, sA);
-    mask(sA, k_lo);
-    auto pstep = [&](int j, int slot, f32x16 (&sc)[2], f32x16 (&sn)[2]) __attribute__((always_inline)) {
-      wait_vmcnt<4>();  // this wave's loads of tile j + 1 have landed (one younger tile in flight)
-      lds_barrier();    // ... and every wave's; every wave is done with step j - 1
-      issue(j + 3, (slot + 3) & 3);
+    // Barrier instance i (once per step for every wave): tile i has landed in every
+    // wave's view, and every wave is done with the LDS reads of steps before i - 1
+    // (K of i - 1, V of i - 2), so tile i + 2 goes into slot (i + 2) % 4 right after it.
+    // Waves 0-3 pass instance j just before step j's MFMA phase; waves 4-7 pass it in
+    // the prologue (j = 0) or just before step j - 1's VALU phase. Both groups pass
+    // ceil4(ntiles) + 1 instances.
+    const int grp = __builtin_amdgcn_readfirstlane(wave >> 2);
+    u32x4 P[4];
+    f32x16 s[2];
+    bool prev_active = false;
+    auto pstep = [&](int j, int slot, const int mode) __attribute__((always_inline)) {
+      if (grp == 0) {
+        wait_vmcnt<4>();  // this wave's loads of tile j have landed (tile j + 1 in flight)
+        lds_barrier();
+        issue(j + 2, (slot + 2) & 3, mode);
+      }
+      if (prev_active) pv(P, (slot + 3) & 3);  // PV of tile j - 1
       const int kb = k_lo + j * KT;
-      pipe_step(sc, sn, slot, (slot + 1) & 3, kb, j < ntiles && kb < lim_max);
-      mask(sn, kb + KT);
+      const bool act = j < ntiles && kb < lim_max;  // wave-uniform
+      if (act) qk(slot, s);
+      if (grp == 1) {
+        wait_vmcnt<4>();  // this wave's loads of tile j + 1 have landed (tile j + 2 in flight)
+        lds_barrier();    // instance j + 1
+        issue(j + 3, (slot + 3) & 3, mode);
+      }
+      if (act) softmax_p(s, kb, P);
+      prev_active = act;
     };
-    for (int j = 0; j < ntiles; j += 4) {
-      pstep(j, 0, sA, sB);
-      pstep(j + 1, 1, sB, sA);
-      pstep(j + 2, 2, sA, sB);
-      pstep(j + 3, 3, sB, sA);
-    }
+    auto prun = [&](const int mode) __attribute__((always_inline)) {
+      if (grp == 1) {  // instance 0 (tiles 0 and 1 were waited for above)
+        lds_barrier();
+        issue(2, 2, mode);
+      }
+      for (int j = 0; j < ntiles; j += 4) {
+        pstep(j, 0, mode);
+        pstep(j + 1, 1, mode);
+        pstep(j + 2, 2, mode);
+        pstep(j + 3, 3, mode);
+      }
+      if (grp == 0) lds_barrier();  // the last instance
+    };
+    if (src_mode == 0) prun(0);
+    else if (src_mode == 1) prun(1);
+    else prun(2);
+    if (prev_active) pv(P, ((ntiles + 3) / 4 * 4 - 1) & 3);  // PV of the last step's tile
     wait_vmcnt<0>();  // no load may land in LDS after the workgroup ends
   }
 

@@ -156,28 +156,29 @@ struct GatherArgs {
 // VPL = 16-byte vectors per lane (the whole row stays in registers). The norm form is a
 // template parameter, so the per-element code is straight-line. Outputs are written once
 // and not read again by this kernel: non-temporal (streaming) stores.
+//
+// The arguments the index load and the row address need come first, as scalars: with
+// kernel-argument preloading they arrive in SGPRs at wave launch, so the index load
+// is the first memory access (the rest of the arguments load beside it).
 template <typename T, int WK, bool CAST, bool GATHERED, int VPL>
-__global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const GatherArgs a) {
+__global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const int64_t* idx, int64_t is_b,
+                                                                 const void* hidden, int64_t hs_b, int64_t hs_s,
+                                                                 int T_rows, int S_rows, const GatherArgs a) {
   constexpr int N = Vec16<T>::N;
   const int lane = threadIdx.x & (kWave - 1);
   // grid (ceil(T / 4), B): four rows of one sequence per workgroup, no division; the row
   // is wave-uniform, so its index, bounds check and addresses live in scalar registers
   const int b = blockIdx.y;
   const int t = static_cast<int>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  if (t >= a.T) return;
+  if (t >= T_rows) return;
+  const int64_t src = idx[b * is_b + t];
   const int nvec = a.H / N;
-  // every address but the source row's is formed before the index arrives
-  const int64_t row = static_cast<int64_t>(b) * a.T + t;
-  const T* hbase = static_cast<const T*>(a.hidden) + b * a.hs_b;
+  const int64_t row = static_cast<int64_t>(b) * T_rows + t;
+  const T* hbase = static_cast<const T*>(hidden) + b * hs_b;
   u32x4* nrow = reinterpret_cast<u32x4*>(static_cast<T*>(a.normed) + row * a.H);
   u32x4* grow = GATHERED ? reinterpret_cast<u32x4*>(static_cast<T*>(a.gathered) + row * a.H) : nullptr;
-  const int64_t hs_s = a.hs_s;
-  // keep the row base and stride in registers ahead of the index load, so the row
-  // address is one multiply-add once the index arrives
-  __asm__ volatile("" : : "s"(hbase), "s"(hs_s));
-  const int64_t src = a.idx[b * a.is_b + t];
   // an index outside [0, S) gives zero rows (a wave-uniform exit before any row load)
-  if (__builtin_expect(static_cast<uint64_t>(src) >= static_cast<uint64_t>(a.S), 0)) {
+  if (__builtin_expect(static_cast<uint64_t>(src) >= static_cast<uint64_t>(S_rows), 0)) {
     const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int v = 0; v < VPL; ++v) {
@@ -341,7 +342,8 @@ bool launch_gather_vec(const GatherArgs& a, dim3 grid, hipStream_t stream) {
   switch (vpl) {
 #define FDLLM_VPL_CASE(n)                                                                  \
   case n:                                                                                  \
-    gather_rmsnorm_vec_kernel<T, WK, CAST, GATHERED, n><<<grid, dim3(256), 0, stream>>>(a); \
+    gather_rmsnorm_vec_kernel<T, WK, CAST, GATHERED, n><<<grid, dim3(256), 0, stream>>>(  \
+        a.idx, a.is_b, a.hidden, a.hs_b, a.hs_s, a.T, a.S, a);                              \
     return true;
     FDLLM_VPL_CASE(1)
     FDLLM_VPL_CASE(2)

@@ -72,7 +72,9 @@ class ForwardGraphs:
     device memory: the token ids and positions are copied into the graph's static
     inputs before each replay, and the static cache's write position and visible
     lengths live in device tensors (StaticKVCache.kv_write_start / scratch_seqlens).
-    Commits advance host-side state and run eagerly. The first use of a kind runs
+    Commits and the prompt prefill are kinds of their own (the full block, or the
+    prompt, without the block cache); the host only advances the committed length
+    after the replay. The first use of a kind runs
     it eagerly once (on the capture stream, so allocations and the attention
     workspace exist before capture), captures it, and replays it; the eager run and
     the replay write the same cache rows."""
@@ -181,7 +183,22 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
         # ---- prefill (generation_functions.py:557-575)
         if min_len > block_size:
             prefill_len = min_len // block_size * block_size
-            logits = model(x[:, :prefill_len], cache, update_past_key_values=True)
+            if graphs is not None and isinstance(cache, StaticKVCache) and cache.get_seq_length() == 0:
+                # replayed from its own graph, as the commits are: the prompt's rows written
+                # at kv_write_start = 0, every prompt key visible as in the eager call, the
+                # last position's logits kept (the only ones read); the committed length
+                # then advances on the host
+                cache.set_kv_write_start(0)
+                cache.set_scratch_seqlens(prefill_len)
+                cache.prepare_write_idx(prefill_len)
+
+                def prefill_fwd(ids, pos):
+                    return model(ids, cache, cache_position=pos, logits_to_keep=1)
+                logits = graphs(("prefill", prefill_len), prefill_fwd, x[:, :prefill_len],
+                                torch.arange(prefill_len, device=dev))
+                cache.commit_written(prefill_len)
+            else:
+                logits = model(x[:, :prefill_len], cache, update_past_key_values=True)
             stats.forwards += 1
             if progress is not None:
                 progress(stats)
@@ -280,8 +297,18 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
                     mask = x[:, blk] == mask_id
                     left = bool((mask[:, s0:s1] & ~finished[:, None]).any())
                     first_masked = bool(mask[:, s0].any())
-            # ---- commit (generation_functions.py:685-696)
-            logits = model(x[:, blk], cache, update_past_key_values=True)
+            # ---- commit (generation_functions.py:685-696). With graphs, the commit is the
+            # full-block forward over the final tokens without the block cache, replayed
+            # from its own graph: it writes the block's rows at kv_write_start (the
+            # committed length while the block is open) and attends over the same keys
+            # as the eager commit; the committed length then advances on the host.
+            if graphs is not None and isinstance(cache, StaticKVCache):
+                def commit_fwd(ids, pos):
+                    return model(ids, cache, cache_position=pos, logits_to_keep=block_size)
+                logits = graphs(("commit",), commit_fwd, x[:, blk], cache_pos)
+                cache.commit_written(block_size)
+            else:
+                logits = model(x[:, blk], cache, update_past_key_values=True)
             stats.forwards += 1
             if progress is not None:
                 progress(stats)

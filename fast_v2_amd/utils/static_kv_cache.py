@@ -116,6 +116,19 @@ class StaticKVCache:
         end = start + seq_len
         return self.key_cache[layer_idx][:, :end], self.value_cache[layer_idx][:, :end]
 
+    def commit_written(self, seq_len: int) -> None:
+        """Commit the ``seq_len`` rows every layer already holds at ``kv_write_start``
+        (written there by a diffusion-step forward over the final tokens of the block,
+        which is what the commit forward computes): advance the committed length as
+        ``update`` does after the last layer (static_kv_cache.py:132-160), without a
+        forward that carries the write position on the host. The caller keeps
+        ``kv_write_start`` at the committed length while the block is open."""
+        if self._seq_len + seq_len > self.max_seq_len:
+            raise RuntimeError(f"StaticKVCache.commit_written: {self._seq_len} + {seq_len} exceeds "
+                               f"max_seq_len {self.max_seq_len}")
+        self._seq_len += seq_len
+        self.cache_seqlens.fill_(self._seq_len)
+
     def __getitem__(self, layer_idx):
         end = self._seq_len
         return self.key_cache[layer_idx][:, :end], self.value_cache[layer_idx][:, :end]
