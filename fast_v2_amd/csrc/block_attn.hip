@@ -56,8 +56,10 @@ constexpr int kMaxDecodeSplits = 16;  // key splits per (sequence, KV head) in t
 #define FDLLM_DECODE_STAGES 2
 #endif
 constexpr int kDecodeStages = FDLLM_DECODE_STAGES;  // tiles in flight per workgroup in the split decode kernel
+// 1: the balanced split kernels number their slots XCD-major (decode_partition); on the
+// bs16 sub-block decode step 27.27 us against 27.75 us in slot order.
 #ifndef FDLLM_XCD_SLOTS
-#define FDLLM_XCD_SLOTS 0
+#define FDLLM_XCD_SLOTS 1
 #endif
 // Waves (x 32 query rows) per prefill workgroup. Measured and not kept: 4 waves (two
 // independent workgroups per CU, so that their softmax and MFMA phases drift apart):
@@ -159,22 +161,47 @@ struct SeqInfo {
   int n_act;   // splits that hold at least one of those keys
 };
 
+// The arguments a kernel's first loads need (lengths, query starts, page table, and the
+// batch and page-table sizes that bound those loads), passed ahead of AttnParams as
+// scalars: with kernel-argument preloading they are in SGPRs when the waves start, so
+// these loads go out without waiting for the argument segment to be read.
+struct Lead {
+  const int* seqlens;
+  const int* q_start;
+  const int32_t* page_table;
+  int B;
+  int max_pages;
+};
+#define FDLLM_LEAD_PARAMS \
+  const int *lead_seqlens, const int *lead_q_start, const int32_t *lead_page_table, int lead_B, int lead_max_pages
+#define FDLLM_LEAD_ARGS(p) (p).seqlens, (p).q_start, (p).page_table, (p).B, (p).max_pages
+#define FDLLM_LEAD_LOCAL const Lead ld{lead_seqlens, lead_q_start, lead_page_table, lead_B, lead_max_pages}
+
+__device__ __forceinline__ Lead lead_of(const AttnParams& p) {
+  return Lead{p.seqlens, p.q_start, p.page_table, p.B, p.max_pages};
+}
+
 template <bool PAGED>
-__device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b, int rb) {
+__device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, const Lead& ld, int b, int rb) {
   SeqInfo si;
   // both loads issue before either is waited for (q_start falls back to a dummy read)
-  int seqlen = p.seqlens[b];
-  const int qs_raw = (p.q_start ? p.q_start : p.seqlens)[b];
+  int seqlen = ld.seqlens[b];
+  const int qs_raw = (ld.q_start ? ld.q_start : ld.seqlens)[b];
   if (seqlen > p.max_seqlen) seqlen = p.max_seqlen;
   if (PAGED && seqlen > p.max_pages * p.page_size) seqlen = p.max_pages * p.page_size;
   if (seqlen < 0) seqlen = 0;
   si.seqlen = seqlen;
-  si.qs = p.q_start ? qs_raw : seqlen - p.Sq;
+  si.qs = ld.q_start ? qs_raw : seqlen - p.Sq;
   const int row0 = rb * p.rows_per_wg;
   const int row_last = min(p.R, row0 + p.rows_per_wg) - 1;  // limits grow with t
   si.kv_end = max(0, row_key_limit(p, seqlen, si.qs, row_last / p.G));
   si.n_act = (si.kv_end + p.chunk - 1) / p.chunk;
   return si;
+}
+
+template <bool PAGED>
+__device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, int b, int rb) {
+  return seq_info<PAGED>(p, lead_of(p), b, rb);
 }
 
 template <int D, int MT, bool F16, bool PAGED>
@@ -802,12 +829,12 @@ __device__ __forceinline__ int active_splits(int t, int n) {
 //     evaluates the same integer search (binary, on one wave's lanes, one lane per
 //     sequence), so all of them agree on the partition.
 template <bool PAGED, int TILE = 32>
-__device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
+__device__ __forceinline__ DecodePart decode_partition(const AttnParams& p, const Lead& ld) {
   DecodePart dp;
   if (p.chunk > 0) {
     dp.b = blockIdx.z;
     dp.split = blockIdx.x;
-    const SeqInfo si = seq_info<PAGED>(p, dp.b, 0);
+    const SeqInfo si = seq_info<PAGED>(p, ld, dp.b, 0);
     const int t = (si.kv_end + TILE - 1) / TILE;
     const int ct = p.chunk / TILE;
     const int n = max(1, min(kMaxDecodeSplits, (t + ct - 1) / ct));
@@ -823,10 +850,10 @@ __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
     return dp;
   }
   const int lane = threadIdx.x & 63;
-  const bool has = lane < p.B;
+  const bool has = lane < ld.B;
   SeqInfo sl;
   sl.seqlen = sl.qs = sl.kv_end = 0;
-  if (has) sl = seq_info<PAGED>(p, lane, 0);
+  if (has) sl = seq_info<PAGED>(p, ld, lane, 0);
   const int t = (sl.kv_end + TILE - 1) / TILE;
   const int S = p.n_splits;
   // splits of a sequence for C tiles per split (an empty sequence still takes one
@@ -836,7 +863,7 @@ __device__ __forceinline__ DecodePart decode_partition(const AttnParams& p) {
   const int T = wave_sum_i32(t);
   // C = ceil(T / S) is a lower bound; ceil(T / (S - B)) fits, as each sequence
   // rounds up by less than one split (the host sizes S so that C = 160 fits).
-  const int nb = min(p.B, 64);
+  const int nb = min(ld.B, 64);
   int lo = min(kDecodeMaxTiles, max(4, ceil_div_small(T, S)));
   int hi = S > nb ? min(kDecodeMaxTiles, max(lo, ceil_div_small(T, S - nb))) : kDecodeMaxTiles;
   while (lo < hi) {
@@ -991,7 +1018,8 @@ __device__ __forceinline__ void merge_splits_n(const AttnParams& p, int b, int k
 //     with one atomic; the last workgroup of the unit merges all partials
 //     (merge_splits) and resets the counter, so no second kernel is launched.
 template <int NS, bool F16, bool PAGED>
-__global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParams p) {
+__global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARAMS, const AttnParams p) {
+  FDLLM_LEAD_LOCAL;
   constexpr int D = 128;
   constexpr int KT = 32;
   constexpr int KS = D + 8;
@@ -1020,17 +1048,17 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
   const int g = lane >> 4;
 
   const int kvh = blockIdx.y;
-  const int n_pt = PAGED ? p.B * p.max_pages : 0;
+  const int n_pt = PAGED ? ld.B * ld.max_pages : 0;
   const bool pt_prefetch = PAGED && n_pt <= kPrefetchPages;  // uniform
   int pf[kPrefetchPages / 512];
   if (pt_prefetch) {
 #pragma unroll
     for (int u = 0; u < kPrefetchPages / 512; ++u) {
       const int idx = tid + 512 * u;
-      pf[u] = idx < n_pt ? p.page_table[idx] : 0;
+      pf[u] = idx < n_pt ? ld.page_table[idx] : 0;
     }
   }
-  const DecodePart dp = decode_partition<PAGED>(p);
+  const DecodePart dp = decode_partition<PAGED>(p, ld);
   if (dp.b < 0) return;  // idle slot (uniform over the workgroup)
   const int b = __builtin_amdgcn_readfirstlane(dp.b);
   const int split = __builtin_amdgcn_readfirstlane(dp.split);
@@ -1070,7 +1098,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(const AttnParam
         if (idx < n_pt) sAllPages[idx] = pf[u];
       }
     } else {
-      const int32_t* pt_row = p.page_table + static_cast<int64_t>(b) * p.max_pages;
+      const int32_t* pt_row = ld.page_table + static_cast<int64_t>(b) * ld.max_pages;
       for (int i = tid; i < ntiles; i += 512) sPage[i] = pt_row[(k_lo + i * KT) >> p.page_shift];
     }
   }
@@ -1361,7 +1389,8 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, c
 //     load latency then sat at the end of every workgroup; its stores alone there
 //     were slower too).
 template <bool F16, bool PAGED, bool SPLIT, bool FUSED, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void kv_prefill_kernel(const AttnParams p) {
+__global__ __launch_bounds__(64 * NW, 2) void kv_prefill_kernel(FDLLM_LEAD_PARAMS, const AttnParams p) {
+  FDLLM_LEAD_LOCAL;
   constexpr int D = 128;
   constexpr int KT = 64;
   constexpr int NT = 64 * NW;      // threads
@@ -1394,7 +1423,7 @@ __global__ __launch_bounds__(64 * NW, 2) void kv_prefill_kernel(const AttnParams
     // one row block of at most 256 rows per (sequence, KV head); keys split as in the
     // split decode kernel, in 64-key tiles
     kvh = blockIdx.y;
-    const DecodePart dp = decode_partition<PAGED, KT>(p);
+    const DecodePart dp = decode_partition<PAGED, KT>(p, ld);
     if (dp.b < 0) return;  // idle slot (uniform over the workgroup)
     b = __builtin_amdgcn_readfirstlane(dp.b);
     split = __builtin_amdgcn_readfirstlane(dp.split);
@@ -1411,7 +1440,7 @@ __global__ __launch_bounds__(64 * NW, 2) void kv_prefill_kernel(const AttnParams
     b = unit / p.Hkv;
     kvh = unit - b * p.Hkv;
     rb = p.n_rb - 1 - static_cast<int>(blockIdx.y);
-    si = seq_info<PAGED>(p, b, rb);
+    si = seq_info<PAGED>(p, ld, b, rb);
     k_lo = 0;
     k_hi = si.kv_end;
     n_act = 1;
@@ -1472,7 +1501,7 @@ __global__ __launch_bounds__(64 * NW, 2) void kv_prefill_kernel(const AttnParams
   }
   const uint16_t* kbase = p.k + kvh * p.k_sh + (PAGED ? 0 : b * p.k_sp);
   const uint16_t* vbase = p.v + kvh * p.v_sh + (PAGED ? 0 : b * p.v_sp);
-  const int32_t* pt_row = PAGED ? p.page_table + static_cast<int64_t>(b) * p.max_pages : nullptr;
+  const int32_t* pt_row = PAGED ? ld.page_table + static_cast<int64_t>(b) * ld.max_pages : nullptr;
   struct Stage {
     u32x4 k[CPT];
     u32x4 v[CPT];
@@ -1899,7 +1928,8 @@ __device__ __forceinline__ void wait_vmcnt() {
 //     side: LDS chunk p of K row r holds column chunk p ^ (r & 15), of V row r
 //     chunk p ^ 4 (r & 3).
 template <bool F16, bool PAGED, bool SPLIT, bool FUSED>
-__global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParams p) {
+__global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARAMS, const AttnParams p) {
+  FDLLM_LEAD_LOCAL;
   constexpr int D = 128;
   constexpr int KT = 64;
   constexpr int NSLOT = 4;
@@ -1923,7 +1953,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParam
   SeqInfo si;
   if constexpr (SPLIT) {
     kvh = blockIdx.y;
-    const DecodePart dp = decode_partition<PAGED, KT>(p);
+    const DecodePart dp = decode_partition<PAGED, KT>(p, ld);
     if (dp.b < 0) return;  // idle slot (uniform over the workgroup)
     b = __builtin_amdgcn_readfirstlane(dp.b);
     split = __builtin_amdgcn_readfirstlane(dp.split);
@@ -1940,7 +1970,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParam
     b = unit / p.Hkv;
     kvh = unit - b * p.Hkv;
     rb = p.n_rb - 1 - static_cast<int>(blockIdx.y);
-    si = seq_info<PAGED>(p, b, rb);
+    si = seq_info<PAGED>(p, ld, b, rb);
     k_lo = 0;
     k_hi = si.kv_end;
     n_act = 1;
@@ -1989,7 +2019,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(const AttnParam
   const int vrow_bytes = static_cast<int>(p.v_ss) * 2;
   const uint16_t* kbase = p.k + kvh * p.k_sh + (PAGED ? 0 : b * p.k_sp);
   const uint16_t* vbase = p.v + kvh * p.v_sh + (PAGED ? 0 : b * p.v_sp);
-  const int32_t* pt_row = PAGED ? p.page_table + static_cast<int64_t>(b) * p.max_pages : nullptr;
+  const int32_t* pt_row = PAGED ? ld.page_table + static_cast<int64_t>(b) * ld.max_pages : nullptr;
   const uint16_t* knbase = FUSED ? p.kn + b * p.n_sb + kvh * p.n_sh : nullptr;
   const uint16_t* vnbase = FUSED ? p.vn + b * p.n_sb + kvh * p.n_sh : nullptr;
   const int nrow_bytes = FUSED ? static_cast<int>(p.n_ss) * 2 : 0;
@@ -2860,20 +2890,20 @@ void launch_prefill(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
                                  : p.max_seqlen;
   if (FDLLM_PREFILL_RING && !SPLIT && (!paged || max_keys + 6 * 64 <= static_cast<int64_t>(kRingMaxHalves) * 32)) {
     if (f16) {
-      if (paged) kv_prefill_ring_kernel<true, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
-      else kv_prefill_ring_kernel<true, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+      if (paged) kv_prefill_ring_kernel<true, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+      else kv_prefill_ring_kernel<true, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
     } else {
-      if (paged) kv_prefill_ring_kernel<false, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
-      else kv_prefill_ring_kernel<false, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(p);
+      if (paged) kv_prefill_ring_kernel<false, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+      else kv_prefill_ring_kernel<false, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
     }
     return;
   }
   if (f16) {
-    if (paged) kv_prefill_kernel<true, true, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(p);
-    else kv_prefill_kernel<true, false, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(p);
+    if (paged) kv_prefill_kernel<true, true, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+    else kv_prefill_kernel<true, false, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(FDLLM_LEAD_ARGS(p), p);
   } else {
-    if (paged) kv_prefill_kernel<false, true, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(p);
-    else kv_prefill_kernel<false, false, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(p);
+    if (paged) kv_prefill_kernel<false, true, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+    else kv_prefill_kernel<false, false, SPLIT, FUSED, NW><<<grid, block, 0, s>>>(FDLLM_LEAD_ARGS(p), p);
   }
 }
 
@@ -3085,11 +3115,11 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
     const bool paged = p.page_table != nullptr;
     const dim3 grid(pl.n_splits, d->num_kv_heads, pl.chunk > 0 ? d->batch : 1);
     if (f16) {
-      if (paged) kv_split_decode_kernel<kDecodeStages, true, true><<<grid, dim3(512), 0, s>>>(p);
-      else kv_split_decode_kernel<kDecodeStages, true, false><<<grid, dim3(512), 0, s>>>(p);
+      if (paged) kv_split_decode_kernel<kDecodeStages, true, true><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+      else kv_split_decode_kernel<kDecodeStages, true, false><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
     } else {
-      if (paged) kv_split_decode_kernel<kDecodeStages, false, true><<<grid, dim3(512), 0, s>>>(p);
-      else kv_split_decode_kernel<kDecodeStages, false, false><<<grid, dim3(512), 0, s>>>(p);
+      if (paged) kv_split_decode_kernel<kDecodeStages, false, true><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+      else kv_split_decode_kernel<kDecodeStages, false, false><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
     }
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }
