@@ -58,6 +58,11 @@ constexpr int kMaxDecodeSplits = 16;  // key splits per (sequence, KV head) in t
 constexpr int kDecodeStages = FDLLM_DECODE_STAGES;  // tiles in flight per workgroup in the split decode kernel
 // 1: the balanced split kernels number their slots XCD-major (decode_partition); on the
 // bs16 sub-block decode step 27.27 us against 27.75 us in slot order.
+// 1: the split prefill (full-block) shapes also take kv_prefill_ring_kernel (bs16
+// full-block step 47.14 us against 47.7 us with kv_prefill_kernel).
+#ifndef FDLLM_PREFILL_RING_SPLIT
+#define FDLLM_PREFILL_RING_SPLIT 1
+#endif
 #ifndef FDLLM_XCD_SLOTS
 #define FDLLM_XCD_SLOTS 1
 #endif
@@ -1350,6 +1355,33 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, c
   }
 }
 
+// Partial (O, m, l) of one split of the split prefill kernels (one row block of at most
+// 256 rows per (sequence, KV head), keys split): the unnormalised rows go to the split's
+// workspace slot (slot rows = the workgroup's rows) for kv_split_prefill_merge_kernel,
+// which follows on the stream. Measured and not kept: the merge in the last-arriving
+// workgroup of each unit, as the split decode kernel does it (full-block step 50.3 us
+// against 45.7 us: one workgroup folding 224 rows of four or five splits is a serial
+// tail longer than the merge kernel and its launch).
+__device__ __forceinline__ void split_prefill_partial(const AttnParams& p, int64_t slot0, int split, int r, int h,
+                                                      const f32x16 (&acc)[4], float m_run, float l_run) {
+  constexpr int D = 128;
+  if (r < p.R) {
+    const int64_t slot = slot0 + split;
+    const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot * 256 * D, 0, 256 * D * 4, kBufferFlags);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        __builtin_amdgcn_raw_buffer_store_b128(
+            __builtin_bit_cast(u32x4, f32x4{acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]}),
+            orsrc, (r * D + 32 * dt + 8 * i + 4 * h) * 4, 0, 0);
+    if (h == 0) {
+      const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot * 256, 0, 256 * 8, kBufferFlags);
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)), mrsrc, r * 8, 0, 0);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Prefill attention: many query rows per KV head (block-causal prefill and
 // commit forwards), head_dim 128, no key split.
@@ -1823,30 +1855,13 @@ __global__ __launch_bounds__(64 * NW, 2) void kv_prefill_kernel(FDLLM_LEAD_PARAM
   l_run = halves_sum(l_run);
   if constexpr (SPLIT) {
     // the unit's (first slot, splits) for the merge kernel, rewritten on every call by
-    // the workgroup of split 0 (every unit has one)
+    // the workgroup of split 0: every unit has one, also a unit of a single split,
+    // which the merge kernel then skips (its entry must not be left from an earlier call)
     if (split == 0 && tid == 0 && p.ws_unit != nullptr) p.ws_unit[b * p.Hkv + kvh] = make_int2(first, n_act);
-  }
-  if (SPLIT && n_act > 1) {
-    // partial (O, m, l) of this key range: slot rows = the workgroup's 256 rows; the
-    // merge kernel that follows on the stream folds them
-    const int64_t slot0 = first;
-    if (r < p.R) {
-      const int64_t slot = slot0 + split;
-      const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot * 256 * D, 0, 256 * D * 4, kBufferFlags);
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(u32x4, f32x4{acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]}),
-              orsrc, (r * D + 32 * dt + 8 * i + 4 * h) * 4, 0, 0);
-      if (h == 0) {
-        const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot * 256, 0, 256 * 8, kBufferFlags);
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)), mrsrc, r * 8, 0,
-                                              0);
-      }
+    if (n_act > 1) {
+      split_prefill_partial(p, first, split, r, h, acc, m_run, l_run);
+      return;
     }
-    return;
   }
   if (r < p.R) {
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
@@ -2465,27 +2480,14 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
   // ---- epilogue: rows of both lane halves are whole after the exchange of l
   l_run = halves_sum(l_run);
   if constexpr (SPLIT) {
+    // the unit's (first slot, splits) for the merge kernel, rewritten on every call by
+    // the workgroup of split 0: every unit has one, also a unit of a single split,
+    // which the merge kernel then skips (its entry must not be left from an earlier call)
     if (split == 0 && tid == 0 && p.ws_unit != nullptr) p.ws_unit[b * p.Hkv + kvh] = make_int2(first, n_act);
-  }
-  if (SPLIT && n_act > 1) {
-    const int64_t slot0 = first;
-    if (r < p.R) {
-      const int64_t slot = slot0 + split;
-      const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + slot * 256 * D, 0, 256 * D * 4, kBufferFlags);
-#pragma unroll
-      for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          __builtin_amdgcn_raw_buffer_store_b128(
-              __builtin_bit_cast(u32x4, f32x4{acc[dt][4 * i], acc[dt][4 * i + 1], acc[dt][4 * i + 2], acc[dt][4 * i + 3]}),
-              orsrc, (r * D + 32 * dt + 8 * i + 4 * h) * 4, 0, 0);
-      if (h == 0) {
-        const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + slot * 256, 0, 256 * 8, kBufferFlags);
-        __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m_run, l_run)), mrsrc, r * 8, 0,
-                                              0);
-      }
+    if (n_act > 1) {
+      split_prefill_partial(p, first, split, r, h, acc, m_run, l_run);
+      return;
     }
-    return;
   }
   if (r < p.R) {
     const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
@@ -2888,7 +2890,8 @@ void launch_prefill(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
   const dim3 block(64 * NW);
   const int64_t max_keys = paged ? std::min<int64_t>(p.max_seqlen, static_cast<int64_t>(p.max_pages) * p.page_size)
                                  : p.max_seqlen;
-  if (FDLLM_PREFILL_RING && !SPLIT && (!paged || max_keys + 6 * 64 <= static_cast<int64_t>(kRingMaxHalves) * 32)) {
+  if (FDLLM_PREFILL_RING && (!SPLIT || FDLLM_PREFILL_RING_SPLIT) &&
+      (!paged || max_keys + 6 * 64 <= static_cast<int64_t>(kRingMaxHalves) * 32)) {
     if (f16) {
       if (paged) kv_prefill_ring_kernel<true, true, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
       else kv_prefill_ring_kernel<true, false, SPLIT, FUSED><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
