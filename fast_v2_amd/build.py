@@ -19,6 +19,10 @@ REPO_DIR = PKG_DIR.parent
 CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "lib"
 LIB_PATH = LIB_DIR / "libfdllm_hip.so"
+# The same sources with FDLLM_TIMELINE: the split decode kernel also writes per-workgroup
+# phase stamps (fast_v2_amd.timeline reads them). A profiling build, never loaded by
+# default.
+TIMELINE_LIB_PATH = LIB_DIR / "libfdllm_hip_timeline.so"
 HEADER = REPO_DIR / "include" / "fdllm_hip.h"
 
 SOURCES = [CSRC / "gather_rmsnorm.hip", CSRC / "block_attn.hip", CSRC / "rope_kv.hip", CSRC / "sampler.hip"]
@@ -58,26 +62,39 @@ def needs_build() -> bool:
     return any(p.stat().st_mtime > built for p in DEPS)
 
 
-def build(force: bool = True, verbose: bool = False) -> Path:
-    """Compile every HIP source into one shared library; returns its path."""
+def build(force: bool = True, verbose: bool = False, timeline: bool = True) -> Path:
+    """Compile every HIP source into one shared library (and, with ``timeline``, the
+    instrumented profiling build beside it, compiled concurrently); returns the path
+    of the production library."""
     if not force and not needs_build():
         return LIB_PATH
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB_PATH.with_suffix(f".so.tmp{os.getpid()}")
-    cmd = [hipcc_path(), *HIPCC_FLAGS, "-I", str(REPO_DIR / "include"),
-           *[str(s) for s in SOURCES], "-o", str(tmp)]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    proc = subprocess.run(cmd, capture_output=True, text=True)
+    jobs = [(LIB_PATH, [])]
+    if timeline:
+        jobs.append((TIMELINE_LIB_PATH, ["-DFDLLM_TIMELINE=1"]))
+    procs = []
+    for path, extra in jobs:
+        tmp = path.with_suffix(f".so.tmp{os.getpid()}")
+        cmd = [hipcc_path(), *HIPCC_FLAGS, *extra, "-I", str(REPO_DIR / "include"),
+               *[str(s) for s in SOURCES], "-o", str(tmp)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        procs.append((path, tmp, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
     # hipcc's host pass does not know the packed-fp32 target feature; that warning is expected.
     noise = "'-packed-fp32-ops' is not a recognized feature"
-    msgs = [l for l in (proc.stderr or "").splitlines() if noise not in l]
-    if proc.returncode != 0:
-        tmp.unlink(missing_ok=True)
-        raise RuntimeError("hipcc failed:\n" + "\n".join(msgs))
-    if verbose and msgs:
-        print("\n".join(msgs), file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
+    errors = []
+    for path, tmp, proc in procs:
+        _, err = proc.communicate()
+        msgs = [l for l in (err or "").splitlines() if noise not in l]
+        if proc.returncode != 0:
+            tmp.unlink(missing_ok=True)
+            errors.append(f"hipcc failed for {path.name}:\n" + "\n".join(msgs))
+            continue
+        if verbose and msgs:
+            print("\n".join(msgs), file=sys.stderr)
+        os.replace(tmp, path)
+    if errors:
+        raise RuntimeError("\n".join(errors))
     return LIB_PATH
 
 

@@ -60,6 +60,9 @@ constexpr int kDecodeStages = FDLLM_DECODE_STAGES;  // tiles in flight per workg
 // bs16 sub-block decode step 27.27 us against 27.75 us in slot order.
 // 1: the split prefill (full-block) shapes also take kv_prefill_ring_kernel (bs16
 // full-block step 47.14 us against 47.7 us with kv_prefill_kernel).
+#ifndef FDLLM_TIMELINE
+#define FDLLM_TIMELINE 0
+#endif
 #ifndef FDLLM_PREFILL_RING_SPLIT
 #define FDLLM_PREFILL_RING_SPLIT 1
 #endif
@@ -103,7 +106,28 @@ struct AttnParams {
   const uint16_t* vn;
   int64_t n_sb, n_ss, n_sh;
   int cap;
+#if FDLLM_TIMELINE
+  uint64_t* tl;  // per-workgroup phase stamps (kTimelineStamps each), or null
+#endif
 };
+
+// Phase stamps of the instrumented build (FDLLM_TIMELINE, built as a library of its
+// own): thread 0 of each workgroup of the split decode kernel writes the device's
+// constant 100 MHz clock (s_memrealtime) at the ends of its phases into the buffer
+// given to fdllm_timeline_attach, kTimelineStamps words per workgroup, indexed by the
+// linear workgroup id. The production library has none of this code.
+constexpr int kTimelineStamps = 8;
+#if FDLLM_TIMELINE
+#define FDLLM_STAMP(i, value)                                                                              \
+  do {                                                                                                     \
+    if (threadIdx.x == 0 && p.tl != nullptr)                                                               \
+      p.tl[(blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z)) * kTimelineStamps + (i)] = (value); \
+  } while (0)
+#else
+#define FDLLM_STAMP(i, value) \
+  do {                        \
+  } while (0)
+#endif
 
 template <bool F16>
 __device__ __forceinline__ f32x4 mfma16x16x32(const u32x4& a, const u32x4& b, const f32x4& c) {
@@ -1025,6 +1049,7 @@ __device__ __forceinline__ void merge_splits_n(const AttnParams& p, int b, int k
 template <int NS, bool F16, bool PAGED>
 __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARAMS, const AttnParams p) {
   FDLLM_LEAD_LOCAL;
+  FDLLM_STAMP(0, __builtin_amdgcn_s_memrealtime());  // start
   constexpr int D = 128;
   constexpr int KT = 32;
   constexpr int KS = D + 8;
@@ -1064,6 +1089,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
     }
   }
   const DecodePart dp = decode_partition<PAGED>(p, ld);
+  FDLLM_STAMP(1, __builtin_amdgcn_s_memrealtime());  // partition known
   if (dp.b < 0) return;  // idle slot (uniform over the workgroup)
   const int b = __builtin_amdgcn_readfirstlane(dp.b);
   const int split = __builtin_amdgcn_readfirstlane(dp.split);
@@ -1240,6 +1266,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   auto step = [&](Stage& sg, int j) {
     store_tile(sg, j & 1);
     lds_barrier();
+    if (FDLLM_TIMELINE && j == 0) FDLLM_STAMP(2, __builtin_amdgcn_s_memrealtime());  // first tiles in LDS
     load_tile(sg, j + 2);
     const int t = 2 * j + team;
     if (t < ntiles) compute_tile(j & 1, k_lo + t * KT);  // wave-uniform
@@ -1253,6 +1280,9 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
     }
   }
 
+  FDLLM_STAMP(3, __builtin_amdgcn_s_memrealtime());  // key loop done
+  FDLLM_STAMP(6, (static_cast<uint64_t>(b) << 48) | (static_cast<uint64_t>(split) << 32) |
+                     (static_cast<uint64_t>(n_act) << 16) | static_cast<uint64_t>(ntiles));
   // ---- merge the two teams: team 1 hands (m, l, O) to team 0 through LDS
   float* xfer = reinterpret_cast<float*>(&sKV[0][0][0]);  // [4 waves][64 lanes][NDT * 4 + 2]
   constexpr int XS = NDT * 4 + 2;
@@ -1298,6 +1328,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
         *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) = u32x2{pack2<F16>(o[0], o[1]), pack2<F16>(o[2], o[3])};
       }
     }
+    FDLLM_STAMP(4, __builtin_amdgcn_s_memrealtime());  // output written (single split)
     return;
   }
   const int unit = b * p.Hkv + kvh;
@@ -1325,9 +1356,11 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   if (tid == 0)
     s_last = __hip_atomic_fetch_add(&p.ws_cnt[unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_act - 1;
   __syncthreads();
+  FDLLM_STAMP(4, __builtin_amdgcn_s_memrealtime());  // partial stored, arrival counted
   if (!s_last) return;
   merge_splits_n<F16>(p, b, kvh, slot0, n_act, tid, 512);
   if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+  FDLLM_STAMP(5, __builtin_amdgcn_s_memrealtime());  // merge written (last arrival)
 }
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
@@ -1788,6 +1821,7 @@ __global__ __launch_bounds__(64 * NW, 2) void kv_prefill_kernel(FDLLM_LEAD_PARAM
   auto step = [&](Stage& sg, int j) {
     store_tile(sg, j & 1);
     lds_barrier();
+    if (FDLLM_TIMELINE && j == 0) FDLLM_STAMP(2, __builtin_amdgcn_s_memrealtime());  // first tiles in LDS
     load_tile(sg, j + 2);
     const int kb = k_lo + j * KT;
     if (j < ntiles && kb < lim_max) compute_tile(j & 1, kb);  // wave-uniform
@@ -2992,6 +3026,10 @@ namespace {
 
 // Validates `d` against its plan and launches the kernels on `stream`, with the
 // caller's workspace or the library's scratch (see fdllm_kv_attn_fwd_noalloc).
+#if FDLLM_TIMELINE
+uint64_t* g_timeline = nullptr;  // device buffer of the phase stamps (instrumented build only)
+#endif
+
 int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace, size_t workspace_bytes,
                    void* stream) {
   if (d->batch == 0 || d->q_len == 0) return FDLLM_OK;
@@ -3061,6 +3099,9 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
   p.cap = d->page_table ? static_cast<int>(std::min<int64_t>(static_cast<int64_t>(d->max_pages) * d->page_size,
                                                               int64_t{1} << 30))
                         : d->max_seqlen;
+#if FDLLM_TIMELINE
+  p.tl = g_timeline;
+#endif
   if (p.kn != nullptr) {
     FDLLM_CHECK_ARG(aligned16(d->k_new) && aligned16(d->v_new) && d->new_stride_b % 8 == 0 &&
                         d->new_stride_s % 8 == 0 && d->new_stride_h % 8 == 0,
@@ -3243,6 +3284,17 @@ extern "C" int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* d, void* workspace, s
   if (rc != FDLLM_OK) return rc;
   return kv_attn_launch(d, pl, workspace, workspace_bytes, stream);
 }
+
+#if FDLLM_TIMELINE
+// Instrumented build only (not part of include/fdllm_hip.h): later attention calls
+// write their split decode kernel's phase stamps, 8 uint64 words per workgroup
+// (linear workgroup id), into `stamps` (device memory; null detaches). The caller
+// sizes it for the grid and clears it before a call.
+extern "C" int fdllm_timeline_attach(void* stamps) {
+  fdllm::g_timeline = static_cast<uint64_t*>(stamps);
+  return FDLLM_OK;
+}
+#endif
 
 extern "C" int fdllm_kv_attn_fwd_noalloc(const fdllm_kv_attn_desc* d, void* stream) {
   using namespace fdllm;
