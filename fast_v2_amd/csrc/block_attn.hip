@@ -2401,9 +2401,13 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
 
   // ---- main loop: tile j in slot j % 4; tiles j + 1, j + 2 in flight; tile j + 3
   // issued into the slot step j - 1 read, after the barrier that ends that step
+  // The first tiles (0-2 here, 0-1 in the ping-pong form) are covered by the full wait
+  // after the prologue, so their steps skip the count wait: the owned rows' stores
+  // (FUSED) are issued after that wait, count in vmcnt like loads and are older than
+  // every later tile, so a count wait there would wait for their acknowledgement.
   auto step = [&](int j, int slot, const int mode) __attribute__((always_inline)) {
-    wait_vmcnt<8>();  // this wave's loads of tile j have landed (two younger tiles in flight)
-    lds_barrier();    // ... and every wave's; every wave is done with step j - 1
+    if (j >= 3) wait_vmcnt<8>();  // this wave's loads of tile j have landed (two younger tiles in flight)
+    lds_barrier();                // ... and every wave's; every wave is done with step j - 1
     issue(j + 3, (slot + 3) & 3, mode);
     const int kb = k_lo + j * KT;
     if (j < ntiles && kb < lim_max) compute_tile(slot, kb);  // wave-uniform
@@ -2475,7 +2479,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
     bool prev_active = false;
     auto pstep = [&](int j, int slot, const int mode) __attribute__((always_inline)) {
       if (grp == 0) {
-        wait_vmcnt<4>();  // this wave's loads of tile j have landed (tile j + 1 in flight)
+        if (j >= 2) wait_vmcnt<4>();  // this wave's loads of tile j have landed (tile j + 1 in flight)
         lds_barrier();
         issue(j + 2, (slot + 2) & 3, mode);
       }
@@ -2484,8 +2488,8 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
       const bool act = j < ntiles && kb < lim_max;  // wave-uniform
       if (act) qk(slot, s);
       if (grp == 1) {
-        wait_vmcnt<4>();  // this wave's loads of tile j + 1 have landed (tile j + 2 in flight)
-        lds_barrier();    // instance j + 1
+        if (j >= 1) wait_vmcnt<4>();  // this wave's loads of tile j + 1 have landed (tile j + 2 in flight)
+        lds_barrier();                // instance j + 1
         issue(j + 3, (slot + 3) & 3, mode);
       }
       if (act) softmax_p(s, kb, P);
