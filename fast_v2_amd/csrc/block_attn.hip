@@ -1388,6 +1388,92 @@ __device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, c
   }
 }
 
+// fp32 attention: fp32 inputs, fp32 output, fp32 arithmetic throughout (the reference's
+// CPU path runs the SDPA shim in fp32, e.g. a 12 / 2-head, 128-dim block of 32 queries over
+// 544 keys; tests/test_focus.py:205-228). Every mask mode, contiguous or paged, any GQA.
+// One wave per (sequence, query token, query head): for the scores lane = key of a 64-key
+// chunk (each lane a full dot product from its key row, the query row broadcast from
+// LDS); for the output lane = head dimension (DPL of them), the chunk's probabilities
+// taken lane by lane with readlane. Online softmax in base 2 (scores pre-multiplied by
+// scale * log2 e), rescaled whenever the chunk maximum moves it.
+template <int DPL, bool PAGED>
+__global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
+  constexpr int D = 64 * DPL;
+  __shared__ __attribute__((aligned(16))) float sq[4][D];
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int b = blockIdx.y;
+  const int rows = p.Sq * p.Hq;
+  const int row = static_cast<int>(blockIdx.x) * 4 + w;  // t * Hq + hq
+  const bool live = row < rows;                           // wave-uniform
+  const int rr = live ? row : rows - 1;
+  const int t = rr / p.Hq;
+  const int hq = rr - t * p.Hq;
+  const int kvh = hq / p.G;
+  int seqlen = p.seqlens[b];
+  if (seqlen > p.max_seqlen) seqlen = p.max_seqlen;
+  if (PAGED && seqlen > p.max_pages * p.page_size) seqlen = p.max_pages * p.page_size;
+  if (seqlen < 0) seqlen = 0;
+  const int qs = p.q_start ? p.q_start[b] : seqlen - p.Sq;
+  const int lim = __builtin_amdgcn_readfirstlane(row_key_limit(p, seqlen, qs, t));
+  const float* q = reinterpret_cast<const float*>(p.q) + b * p.q_sb + t * p.q_ss + hq * p.q_sh;
+  for (int i = lane; i < D; i += 64) sq[w][i] = q[i];
+  __syncthreads();
+  const float* kb = reinterpret_cast<const float*>(p.k) + kvh * p.k_sh;
+  const float* vb = reinterpret_cast<const float*>(p.v) + kvh * p.v_sh;
+  auto row_off = [&](int key, bool kcache) -> int64_t {
+    const int64_t ss = kcache ? p.k_ss : p.v_ss;
+    if constexpr (PAGED) {
+      const int page = p.page_table[static_cast<int64_t>(b) * p.max_pages + (key >> p.page_shift)];
+      return static_cast<int64_t>(page) * (kcache ? p.k_sp : p.v_sp) + (key & (p.page_size - 1)) * ss;
+    } else {
+      return static_cast<int64_t>(b) * (kcache ? p.k_sp : p.v_sp) + static_cast<int64_t>(key) * ss;
+    }
+  };
+  float o[DPL];
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) o[j] = 0.f;
+  float m = -INFINITY, l = 0.f;
+  for (int k0 = 0; k0 < lim; k0 += 64) {
+    const int key = k0 + lane;
+    float s = -INFINITY;
+    if (key < lim) {
+      const float* kr = kb + row_off(key, true);
+      float acc = 0.f;
+#pragma unroll 8
+      for (int i = 0; i < D; i += 4) {
+        const f32x4 kv = *reinterpret_cast<const f32x4*>(kr + i);
+        const f32x4 qv = *reinterpret_cast<const f32x4*>(&sq[w][i]);
+        acc = fmaf(qv[0], kv[0], acc);
+        acc = fmaf(qv[1], kv[1], acc);
+        acc = fmaf(qv[2], kv[2], acc);
+        acc = fmaf(qv[3], kv[3], acc);
+      }
+      s = acc * p.scale_log2;
+    }
+    const float m_new = fmaxf(m, wave_allreduce_max(s));
+    const float alpha = m == -INFINITY ? 0.f : fast_exp2(m - m_new);
+    const float pk = key < lim ? fast_exp2(s - m_new) : 0.f;
+    l = l * alpha + wave_allreduce_sum(pk);
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) o[j] *= alpha;
+    const int nk = min(64, lim - k0);
+    for (int kk = 0; kk < nk; ++kk) {
+      const float pkk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pk), kk));
+      const float* vr = vb + row_off(k0 + kk, false);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) o[j] = fmaf(pkk, vr[lane + 64 * j], o[j]);
+    }
+    m = m_new;
+  }
+  if (live) {
+    float* out = reinterpret_cast<float*>(p.out) + b * p.o_sb + t * p.o_ss + hq * p.o_sh;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) out[lane + 64 * j] = o[j] * inv;
+  }
+}
+
 // Partial (O, m, l) of one split of the split prefill kernels (one row block of at most
 // 256 rows per (sequence, KV head), keys split): the unnormalised rows go to the split's
 // workspace slot (slot rows = the workgroup's rows) for kv_split_prefill_merge_kernel,
@@ -2683,7 +2769,14 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const KVWriteArgs a) {
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 // Kernel families a call can take (make_plan picks one per descriptor).
-enum PlanKind { kPlanGeneral = 0, kPlanAllHeads = 1, kPlanSplitDecode = 2, kPlanPrefill = 3, kPlanSplitPrefill = 4 };
+enum PlanKind {
+  kPlanGeneral = 0,
+  kPlanAllHeads = 1,
+  kPlanSplitDecode = 2,
+  kPlanPrefill = 3,
+  kPlanSplitPrefill = 4,
+  kPlanF32 = 5
+};
 
 struct Plan {
   int kind;     // PlanKind
@@ -2704,8 +2797,8 @@ constexpr size_t kCounterBytes = 64 * 1024;           // arrival counters at the
 int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
   FDLLM_CHECK_ARG(d != nullptr, "fdllm_kv_attn: null descriptor");
   pl->ws_unit_off = 0;
-  FDLLM_CHECK_ARG(d->dtype == FDLLM_DTYPE_BF16 || d->dtype == FDLLM_DTYPE_F16,
-                  "fdllm_kv_attn: dtype %d unsupported (bf16 or fp16 only)", d->dtype);
+  FDLLM_CHECK_ARG(d->dtype == FDLLM_DTYPE_BF16 || d->dtype == FDLLM_DTYPE_F16 || d->dtype == FDLLM_DTYPE_F32,
+                  "fdllm_kv_attn: dtype %d unsupported (bf16, fp16 or fp32)", d->dtype);
   FDLLM_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128, "fdllm_kv_attn: head_dim %d unsupported (64 or 128)",
                   d->head_dim);
   FDLLM_CHECK_ARG(d->batch >= 0 && d->q_len >= 0 && d->num_q_heads > 0 && d->num_kv_heads > 0,
@@ -2717,6 +2810,26 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
                   "fdllm_kv_attn: unknown mask_mode %d", d->mask_mode);
   FDLLM_CHECK_ARG(d->mask_mode != FDLLM_MASK_BLOCK_CAUSAL || d->mask_block > 0,
                   "fdllm_kv_attn: block-causal mask needs mask_block > 0");
+  if (d->dtype == FDLLM_DTYPE_F32) {
+    // fp32: kv_attn_f32_kernel, no workspace, no key split; pages of any power of two
+    FDLLM_CHECK_ARG(d->page_table == nullptr ||
+                        (d->page_size > 0 && (d->page_size & (d->page_size - 1)) == 0 && d->max_pages > 0),
+                    "fdllm_kv_attn: page table needs a power-of-two page_size and max_pages > 0");
+    FDLLM_CHECK_ARG(d->k_new == nullptr && d->v_new == nullptr,
+                    "fdllm_kv_attn: the cache write (k_new / v_new) takes bf16 or fp16 only");
+    const int64_t rows = static_cast<int64_t>(d->q_len) * d->num_q_heads;
+    FDLLM_CHECK_ARG(rows < (int64_t{1} << 31) - 4, "fdllm_kv_attn: q_len * num_q_heads too large");
+    pl->kind = kPlanF32;
+    pl->decode = false;
+    pl->MT = 0;
+    pl->rows_per_wg = 4;
+    pl->n_rb = 1;
+    pl->n_splits = 1;
+    pl->chunk = 0;
+    pl->R = static_cast<int>(std::min<int64_t>(rows, 1 << 30));
+    pl->ws_o_bytes = pl->ws_ml_bytes = 0;
+    return FDLLM_OK;
+  }
   // Each thread stages aligned groups of 2048 / head_dim keys from one page.
   FDLLM_CHECK_ARG(d->page_table == nullptr ||
                       (d->page_size >= kThreads * 8 / std::max(d->head_dim, 8) &&
@@ -3127,6 +3240,20 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
   }
   const bool f16 = d->dtype == FDLLM_DTYPE_F16;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (pl.kind == kPlanF32) {
+    const int64_t rows = static_cast<int64_t>(d->q_len) * d->num_q_heads;
+    FDLLM_CHECK_ARG(d->batch < 65536, "fdllm_kv_attn_fwd: batch too large");
+    const dim3 grid(static_cast<unsigned>((rows + 3) / 4), static_cast<unsigned>(d->batch));
+    const bool paged = d->page_table != nullptr;
+    if (d->head_dim == 128) {
+      if (paged) kv_attn_f32_kernel<2, true><<<grid, dim3(256), 0, s>>>(p);
+      else kv_attn_f32_kernel<2, false><<<grid, dim3(256), 0, s>>>(p);
+    } else {
+      if (paged) kv_attn_f32_kernel<1, true><<<grid, dim3(256), 0, s>>>(p);
+      else kv_attn_f32_kernel<1, false><<<grid, dim3(256), 0, s>>>(p);
+    }
+    FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
+  }
   // Cache write of the call (k_new / v_new): inside the prefill kernels, otherwise as
   // a kernel of its own before the attention, at q_start[b] + t (seqlens[b] - q_len + t)
   const bool fuse_write = p.kn != nullptr && (pl.kind == kPlanPrefill || pl.kind == kPlanSplitPrefill);

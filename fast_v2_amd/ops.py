@@ -228,7 +228,8 @@ def block_attn(
 ) -> torch.Tensor:
     """Attention of BSHD queries over a (paged) BSHD KV cache.
 
-    q            [B, Sq, Hq, D] bf16/fp16 (head_dim contiguous)
+    q            [B, Sq, Hq, D] bf16/fp16, or fp32 (computed in fp32 throughout by a
+                 general kernel; head_dim contiguous)
     k/v_cache    [B, max_S, Hkv, D] without a page table, or the page pool
                  [num_pages, page_size, Hkv, D] with ``page_table`` [B, max_pages] int32
     cache_seqlens [B] visible key count per sequence (int32; other ints converted)
@@ -259,9 +260,12 @@ def block_attn(
     if page_table is not None:
         tensors.append(page_table)
     dev = _require_gpu(*tensors)
-    if not (q.dtype == k_cache.dtype == v_cache.dtype) or q.dtype not in (torch.bfloat16, torch.float16):
-        raise RuntimeError(
-            f"block_attn: q/k/v must share dtype bf16 or fp16 (got {q.dtype}, {k_cache.dtype}, {v_cache.dtype})")
+    if not (q.dtype == k_cache.dtype == v_cache.dtype) or \
+            q.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise RuntimeError(f"block_attn: q/k/v must share dtype bf16, fp16 or fp32 "
+                           f"(got {q.dtype}, {k_cache.dtype}, {v_cache.dtype})")
+    if q.dtype == torch.float32 and k_new is not None:
+        raise RuntimeError("block_attn: the cache write (k_new / v_new) takes bf16 or fp16 only")
     if k_cache.shape != v_cache.shape:
         raise RuntimeError("block_attn: k_cache and v_cache shapes differ")
     B, Sq, Hq, D = q.shape

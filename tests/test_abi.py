@@ -99,7 +99,7 @@ def test_rejected_arguments_launch_nothing(lib):
     """Calls that fail validation return a negative code and set the error text."""
     from fast_v2_amd import _ffi
     d = _ffi.KVAttnDesc()
-    d.dtype = _ffi.DTYPE_F32  # unsupported by the attention kernels
+    d.dtype = 99  # no such dtype
     d.head_dim, d.num_q_heads, d.num_kv_heads = 128, 28, 4
     size = ctypes.c_size_t(0)
     rc = lib.fdllm_kv_attn_workspace_size(ctypes.byref(d), ctypes.byref(size))

@@ -45,6 +45,59 @@ def test_golden_small_decode_bf16(gpu):
     _check(out, z["out"], atol=3e-2, rtol=3e-2)
 
 
+def test_golden_small_decode_fp32(gpu):
+    """Config 1 at its own precision: the fp32 golden (torch CPU SDPA, 1 x 32 queries x
+    12/2 heads over 512 + 32 keys) against the fp32 kernel on the same fp32 inputs, within
+    1e-5 (both accumulate in fp32; only the summation order differs)."""
+    z = np.load(GOLDEN / "kv_decode_small.npz")
+    q, k, v = (torch.from_numpy(z[n]) for n in ("q", "k", "v"))
+    assert q.dtype == k.dtype == v.dtype == torch.float32
+    seq = torch.from_numpy(z["seqlens"])
+    out = ops.block_attn(q.to(gpu), k.to(gpu), v.to(gpu), seq.to(gpu), float(z["scale"]))
+    assert out.dtype == torch.float32
+    np.testing.assert_allclose(out.cpu().numpy(), z["out"], atol=1e-5, rtol=1e-5)
+    # and the float64 brute force of the oracle
+    np.testing.assert_allclose(out.cpu().numpy(), oa.attention_np(q, k, v, seq, float(z["scale"])),
+                               atol=1e-5, rtol=1e-5)
+
+
+@pytest.mark.parametrize("mask_mode", [_ffi.MASK_SEQLEN, _ffi.MASK_CAUSAL, _ffi.MASK_BLOCK_CAUSAL])
+@pytest.mark.parametrize("paged", [False, True])
+def test_fp32_masks_paged_and_gqa(gpu, mask_mode, paged):
+    """fp32 kernel: every mask mode, contiguous and paged caches, GQA 1 / 4 / 8, head_dim
+    64 and 128, ragged and empty lengths, q_start given or not; within 1e-5 of the float64
+    brute force."""
+    g = torch.Generator().manual_seed(100 + 10 * mask_mode + paged)
+    for Hq, Hkv, D, Sq in ((12, 2, 128, 32), (8, 8, 64, 5), (16, 4, 128, 1)):
+        B, S, ps = 3, 160, 16
+        seqlens = torch.tensor([150, 0, 77], dtype=torch.int32)
+        q = torch.randn(B, Sq, Hq, D, generator=g)
+        k = torch.randn(B, S, Hkv, D, generator=g)
+        v = torch.randn(B, S, Hkv, D, generator=g)
+        q_start = torch.tensor([150 - Sq, 0, 40], dtype=torch.int32) if Sq > 1 else None
+        print(f"case fp32 mask={mask_mode} paged={paged} Hq={Hq} Hkv={Hkv} D={D} Sq={Sq}", flush=True)
+        exp = oa.attention_np(q, k, v, seqlens, None, mask_mode=mask_mode, mask_block=32, q_start=q_start)
+        if paged:
+            n_pages = S // ps
+            perm = torch.randperm(B * n_pages, generator=g)
+            pt = perm.view(B, n_pages).to(torch.int32)
+            kp = torch.empty(B * n_pages, ps, Hkv, D)
+            vp = torch.empty_like(kp)
+            for b in range(B):
+                for j in range(n_pages):
+                    kp[pt[b, j]] = k[b, j * ps:(j + 1) * ps]
+                    vp[pt[b, j]] = v[b, j * ps:(j + 1) * ps]
+            out = ops.block_attn(q.to(gpu), kp.to(gpu), vp.to(gpu), seqlens.to(gpu), None, mask_mode=mask_mode,
+                                 mask_block=32, q_start=None if q_start is None else q_start.to(gpu),
+                                 page_table=pt.to(gpu), page_size=ps)
+        else:
+            out = ops.block_attn(q.to(gpu), k.to(gpu), v.to(gpu), seqlens.to(gpu), None, mask_mode=mask_mode,
+                                 mask_block=32, q_start=None if q_start is None else q_start.to(gpu))
+        got = out.cpu().numpy()
+        np.testing.assert_allclose(got, exp, atol=1e-5, rtol=1e-5)
+        assert np.count_nonzero(got[1]) == 0  # the empty sequence
+
+
 @pytest.mark.parametrize("kv_split", [0, 64, 256, 1 << 20])
 def test_paged_subblock_decode_7b_bs16(gpu, kv_split):
     wl = workloads.kv_decode_paged(seed=0)
