@@ -232,3 +232,26 @@ def test_rope_is_a_rotation_of_half_pairs():
     # norms are preserved
     torch.testing.assert_close(ke.norm(dim=-1), k.norm(dim=-1), atol=1e-5, rtol=1e-5)
     assert math.isclose(float(qe.norm()), float(q.norm()), rel_tol=1e-5)
+
+
+def test_timeline_phase_statistics():
+    """fast_v2_amd.timeline.analyse on hand-made stamps (100 MHz ticks): idle slots,
+    single-split units and merging workgroups are told apart, and the phase ends and
+    durations come out in µs from the first start."""
+    import numpy as np
+    from fast_v2_amd import timeline as tlm
+    st = np.zeros((6, tlm.STAMPS), dtype=np.int64)
+    t0 = 1_000_000
+    #                 start  part  first  loop   arrive  merge   info (b, split, n_act, ntiles)
+    st[0, :7] = [t0, t0 + 100, t0 + 400, t0 + 1500, t0 + 1700, t0 + 1950, (0 << 48) | (0 << 32) | (2 << 16) | 20]
+    st[1, :7] = [t0 + 50, t0 + 150, t0 + 450, t0 + 1600, t0 + 1800, 0, (0 << 48) | (1 << 32) | (2 << 16) | 21]
+    st[2, :7] = [t0 + 20, t0 + 130, t0 + 420, t0 + 1200, t0 + 1300, 0, (1 << 48) | (0 << 32) | (1 << 16) | 10]
+    st[3, :2] = [t0 + 30, t0 + 140]  # an idle slot: start and partition only
+    res = tlm.analyse(st)
+    assert res["workgroups"] == 4 and res["active"] == 3 and res["merging"] == 1
+    assert res["tiles_per_workgroup"] == (10.0, 20.0, 21.0)
+    assert res["start"] == (0.0, 0.25, 0.5)
+    assert res["merge written"] == (19.5, 19.5, 19.5)
+    assert math.isclose(res["span"], 19.5)
+    assert np.allclose(res["d_loop"], (7.8, 11.0, 11.5))
+    assert np.allclose(res["d_merge"], (2.5, 2.5, 2.5))
