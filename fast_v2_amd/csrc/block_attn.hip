@@ -112,10 +112,11 @@ struct AttnParams {
 };
 
 // Phase stamps of the instrumented build (FDLLM_TIMELINE, built as a library of its
-// own): thread 0 of each workgroup of the split decode kernel writes the device's
-// constant 100 MHz clock (s_memrealtime) at the ends of its phases into the buffer
-// given to fdllm_timeline_attach, kTimelineStamps words per workgroup, indexed by the
-// linear workgroup id. The production library has none of this code.
+// own): thread 0 of each workgroup of the split decode kernel (and of the ring prefill
+// kernel) writes the device's constant 100 MHz clock (s_memrealtime) at the ends of its
+// phases into the buffer given to fdllm_timeline_attach, kTimelineStamps words per
+// workgroup, indexed by the linear workgroup id. The production library has none of
+// this code.
 constexpr int kTimelineStamps = 8;
 #if FDLLM_TIMELINE
 #define FDLLM_STAMP(i, value)                                                                              \
@@ -2069,6 +2070,7 @@ __device__ __forceinline__ void wait_vmcnt() {
 template <bool F16, bool PAGED, bool SPLIT, bool FUSED>
 __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARAMS, const AttnParams p) {
   FDLLM_LEAD_LOCAL;
+  FDLLM_STAMP(0, __builtin_amdgcn_s_memrealtime());  // start
   constexpr int D = 128;
   constexpr int KT = 64;
   constexpr int NSLOT = 4;
@@ -2093,6 +2095,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
   if constexpr (SPLIT) {
     kvh = blockIdx.y;
     const DecodePart dp = decode_partition<PAGED, KT>(p, ld);
+    FDLLM_STAMP(1, __builtin_amdgcn_s_memrealtime());  // partition known
     if (dp.b < 0) return;  // idle slot (uniform over the workgroup)
     b = __builtin_amdgcn_readfirstlane(dp.b);
     split = __builtin_amdgcn_readfirstlane(dp.split);
@@ -2535,6 +2538,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
     for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * h);
   }
   __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15): vector memory only
+  FDLLM_STAMP(2, __builtin_amdgcn_s_memrealtime());  // first tiles and Q landed (this wave)
   if constexpr (FUSED) {
     own_store(0);
     for (int base = 1024; base < own_n; base += 1024) {  // more than 64 owned rows (GQA < 4)
@@ -2604,6 +2608,9 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
     if (prev_active) pv(P, ((ntiles + 3) / 4 * 4 - 1) & 3);  // PV of the last step's tile
     wait_vmcnt<0>();  // no load may land in LDS after the workgroup ends
   }
+  FDLLM_STAMP(3, __builtin_amdgcn_s_memrealtime());  // key loop done (this wave)
+  FDLLM_STAMP(6, (static_cast<uint64_t>(b) << 48) | (static_cast<uint64_t>(split) << 32) |
+                     (static_cast<uint64_t>(n_act) << 16) | static_cast<uint64_t>(ntiles));
 
   // ---- epilogue: rows of both lane halves are whole after the exchange of l
   l_run = halves_sum(l_run);
@@ -2614,6 +2621,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
     if (split == 0 && tid == 0 && p.ws_unit != nullptr) p.ws_unit[b * p.Hkv + kvh] = make_int2(first, n_act);
     if (n_act > 1) {
       split_prefill_partial(p, first, split, r, h, acc, m_run, l_run);
+      FDLLM_STAMP(4, __builtin_amdgcn_s_memrealtime());  // partial stores issued
       return;
     }
   }
@@ -2630,6 +2638,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
                   pack2<F16>(acc[dt][e + 2] * inv, acc[dt][e + 3] * inv)};
       }
   }
+  FDLLM_STAMP(4, __builtin_amdgcn_s_memrealtime());  // output stores issued
 }
 
 // Merge of the split prefill kernel's partials: grid (row chunks of 32, units),

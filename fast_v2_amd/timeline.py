@@ -18,7 +18,12 @@ pools as the benchmark's decode leg does, so every call reads its K/V from HBM; 
 call is preceded by a clear of the stamp buffer and a synchronisation, so the stamps
 show the kernel alone (no overlap with the previous call's tail).
 
-    python -m fast_v2_amd.timeline [--calls 56] [--layers 28]
+    python -m fast_v2_amd.timeline [--calls 56] [--layers 28] [--full-block]
+
+With --full-block all 32 queries of the block are active (the full-block forward): the
+call runs kv_prefill_ring_kernel in its split form, whose stamps are 0 start, 1
+partition known, 2 first tiles and Q landed, 3 key loop done, 4 partial stores issued,
+then the merge kernel (not stamped).
 """
 from __future__ import annotations
 
@@ -75,6 +80,7 @@ def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--calls", type=int, default=56)
     ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--full-block", action="store_true", help="all 32 block queries active")
     args = ap.parse_args(argv)
     if "fast_v2_amd._ffi" in sys.modules:
         raise RuntimeError("fast_v2_amd.timeline must load the instrumented library before anything else loads "
@@ -93,7 +99,7 @@ def main(argv=None) -> int:
     attach.restype = ctypes.c_int
 
     dev = torch.device("cuda", 0)
-    wl = workloads.kv_decode_paged(seed=0)
+    wl = workloads.kv_decode_paged(seed=0, active=32 if args.full_block else 8)
     layers = args.layers
     gen = torch.Generator(device=dev).manual_seed(1)
     kp = torch.empty((layers,) + tuple(wl.k_pool.shape), dtype=wl.k_pool.dtype, device=dev)
@@ -134,10 +140,13 @@ def main(argv=None) -> int:
         vals = [r[key] if j is None else r[key][j] for r in per_call]
         return float(np.median(vals))
 
-    print(f"# split decode kernel timeline: bs16 sub-block decode step, {args.calls} calls over {layers} layer pools")
+    what = ("ring prefill kernel (split form) timeline: bs16 full-block step" if args.full_block else
+            "split decode kernel timeline: bs16 sub-block decode step")
+    tile = 64 if args.full_block else 32
+    print(f"# {what}, {args.calls} calls over {layers} layer pools")
     print()
     print(f"workgroups {med('workgroups'):.0f}, with keys {med('active'):.0f}, merging {med('merging'):.0f}; "
-          f"tiles of 32 keys per workgroup (min / median / max) {med('tiles_per_workgroup', 0):.0f} / "
+          f"tiles of {tile} keys per workgroup (min / median / max) {med('tiles_per_workgroup', 0):.0f} / "
           f"{med('tiles_per_workgroup', 1):.0f} / {med('tiles_per_workgroup', 2):.0f}")
     print(f"kernel span from the stamps (first start to last end): {med('span'):.2f} us; "
           f"HIP-event time of the same calls (launch from idle included): {float(np.median(event_us)):.2f} us")
