@@ -78,6 +78,42 @@ def _time_graph(torch, step_fn, steps: int, warmup: int) -> float:
     return us
 
 
+def _time_graphs_rotating(torch, step_fns: dict, steps: int, warmup: int, rounds: int = 3) -> dict:
+    """Capture `steps` steps of each function in a graph of its own (after `warmup` eager
+    steps on the capture stream), then time one replay of each in turn, `rounds` times
+    over; returns the median µs per step of each. Interleaving keeps clock and cache
+    state from favouring whichever form would otherwise be timed last."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graphs = {}
+    for name, fn in step_fns.items():
+        with torch.cuda.stream(s):
+            for i in range(warmup):
+                fn(i)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=s):
+            for i in range(steps):
+                fn(i)
+        torch.cuda.synchronize()
+        graphs[name] = g
+    for g in graphs.values():
+        g.replay()
+    torch.cuda.synchronize()
+    times = {name: [] for name in graphs}
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    for _ in range(rounds):
+        for name, g in graphs.items():
+            start.record()
+            g.replay()
+            end.record()
+            torch.cuda.synchronize()
+            times[name].append(start.elapsed_time(end) * 1e3 / steps)
+    del graphs
+    return {name: sorted(t)[len(t) // 2] for name, t in times.items()}
+
+
 def _traffic(name: str):
     try:
         data = json.loads(TRAFFIC_FILE.read_text())
@@ -292,28 +328,38 @@ def bench_prefill(torch, args):
     sl = torch.full((B,), S, dtype=torch.int32, device=dev)
     out = torch.empty_like(q)
 
-    def fused(i):
-        # the whole config-4 call: K/V stored into the cache by the attention kernel itself
+    def whole_call(i):
+        # the whole config-4 call: the K/V rows stored into the cache and the attention, in
+        # one fdllm_kv_attn_fwd (the prefill kernel stores the rows itself)
         ops.block_attn(q, kc, vc, sl, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL, mask_block=wl.block, out=out,
                        k_new=k, v_new=v)
+
+    def copy_kernel_write(i):
+        # the same call with the rows stored by a copy kernel ahead of the prefill kernel
+        ops.block_attn(q, kc, vc, sl, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL, mask_block=wl.block, out=out,
+                       k_new=k, v_new=v, cache_write_kernel=True)
 
     def attn_only(i):
         ops.block_attn(q, kc, vc, sl, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL, mask_block=wl.block, out=out)
 
-    def unfused(i):
-        ops.kv_cache_write(k, v, kc, vc, write_offset=0)
-        attn_only(i)
-
     steps = args.prefill_steps
-    us_full = _time_graph(torch, fused, steps, 2)
+    whole_call(0)
     if not torch.equal(kc, k) or not torch.equal(vc, v):
-        raise RuntimeError("prefill: the fused call left a cache that differs from the new K/V rows")
-    us_attn = _time_graph(torch, attn_only, steps, 2)
-    us_unfused = _time_graph(torch, unfused, steps, 2)
+        raise RuntimeError("prefill: the call left a cache that differs from the new K/V rows")
+    kc.zero_()
+    vc.zero_()
+    copy_kernel_write(0)
+    if not torch.equal(kc, k) or not torch.equal(vc, v):
+        raise RuntimeError("prefill: the copy-kernel cache write left a cache that differs from the new K/V rows")
+    # the three forms timed in rotation (a form timed first, right after other work, ran
+    # 10-15 us slower than in a later slot): three rounds, the median per form
+    us = _time_graphs_rotating(torch, {"call": whole_call, "attn": attn_only, "copy": copy_kernel_write},
+                               steps, 2, rounds=3)
+    us_full, us_attn, us_copy = us["call"], us["attn"], us["copy"]
     flops = workloads.prefill_flops(B, S, Hq, D, wl.block)
     nbytes = workloads.prefill_bytes(B, S, Hq, Hkv, D)
     tf = flops / (us_full * 1e-6) / 1e12
-    res = {"us_per_call": us_full, "us_attention_only": us_attn, "us_write_kernel_then_attention": us_unfused,
+    res = {"us_per_call": us_full, "us_attention_only": us_attn, "us_copy_kernel_then_attention": us_copy,
            "flops": flops, "bytes_with_cache_write": nbytes,
            "roofline": _roofline("mfma", tf, MFMA_BF16_PEAK_TFLOPS, "TFLOP/s", _traffic("kv_attn_prefill_fused")),
            "tflops_attention_only": flops / (us_attn * 1e-6) / 1e12}

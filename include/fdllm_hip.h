@@ -179,6 +179,12 @@ typedef struct fdllm_kv_attn_desc {
 /* Decode shapes: use the all-KV-heads-per-workgroup kernel instead of the
  * split-KV kernel with one KV head per workgroup. */
 #define FDLLM_ATTN_ALL_HEADS_DECODE 2
+/* With k_new / v_new: store the new rows into the cache by a copy kernel launched
+ * before the attention, also for prefill shapes, whose kernels otherwise store them
+ * themselves (each row by the one workgroup that owns it). Same results, bit for bit;
+ * the in-kernel write is the default (the 4 x 4096-token prefill: 473-475 us against
+ * 479-480 us with the copy kernel, timed in rotation). */
+#define FDLLM_ATTN_CACHE_WRITE_KERNEL 4
 
 /* Bytes of device workspace fdllm_kv_attn_fwd needs for `desc` (0 when the call
  * is not split over several workgroups per KV head). The workspace starts with

@@ -220,6 +220,12 @@ def test_block_causal_prefill_full_size_sampled(gpu):
     ref = ops.block_attn(wl.q.to(gpu), ku, vu, seqlens, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL,
                          mask_block=wl.block)
     assert torch.equal(out, ref)
+    # the cache write by the copy kernel (FDLLM_ATTN_CACHE_WRITE_KERNEL): same cache, same output
+    kf, vf = torch.full_like(kc, 7.0), torch.full_like(vc, -7.0)
+    out_f = ops.block_attn(wl.q.to(gpu), kf, vf, seqlens, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL,
+                           mask_block=wl.block, k_new=k, v_new=v, cache_write_kernel=True)
+    assert torch.equal(kf, k) and torch.equal(vf, v)
+    assert torch.equal(out_f, ref)
     out = out.cpu()
     for blk in (0, 1, 63, 64, 127):
         t0 = blk * wl.block
@@ -621,12 +627,15 @@ def test_block_decode_split_prefill_kernel(gpu, case):
     "subblock_fallback",        # 8 queries: split decode kernel, cache write kernel first
     "head64_fallback",          # head_dim 64: the general kernel, cache write kernel first
 ])
-def test_fused_cache_write(gpu, case):
+@pytest.mark.parametrize("in_kernel", [False, True])
+def test_fused_cache_write(gpu, case, in_kernel):
     """k_new / v_new: the call stores the query tokens' K / V rows into the cache at
-    q_start + t and attends over the updated cache. The cache must equal the oracle's
-    write bit for bit, the output must equal the same call made as a separate cache
-    write followed by the attention (bit for bit) and match the float64 oracle over
-    the written cache."""
+    q_start + t and attends over the updated cache, from inside the prefill kernels
+    (in_kernel, where the shape has them) or by its copy kernel
+    (FDLLM_ATTN_CACHE_WRITE_KERNEL). The cache must equal
+    the oracle's write bit for bit, the output must equal the same call made as a
+    separate cache write followed by the attention (bit for bit) and match the float64
+    oracle over the written cache."""
     g = torch.Generator().manual_seed(sum(map(ord, case)))
     dtype, page, mode, blk, D, hq, hkv, explicit_qs = torch.bfloat16, 0, _ffi.MASK_BLOCK_CAUSAL, 32, 128, 28, 4, False
     if case == "prefill_q0_contig":
@@ -649,7 +658,7 @@ def test_fused_cache_write(gpu, case):
         B, Sq, qs, cap, lens, D, hq, hkv = 3, 300, [0, 33, 128], 512, None, 64, 8, 2
     if lens is None:
         lens = [q0 + Sq for q0 in qs]
-    print(f"case fused cache write {case}", flush=True)
+    print(f"case fused cache write {case} in_kernel={in_kernel}", flush=True)
     q = torch.randn(B, Sq, hq, D, generator=g).to(dtype)
     kc0 = torch.randn(B, cap, hkv, D, generator=g).to(dtype)
     vc0 = torch.randn(B, cap, hkv, D, generator=g).to(dtype)
@@ -671,7 +680,7 @@ def test_fused_cache_write(gpu, case):
     qarg = dict(q_start=qst.to(gpu)) if explicit_qs else {}
     kf, vf = kp0.to(gpu), vp0.to(gpu)
     out = ops.block_attn(q.to(gpu), kf, vf, sl.to(gpu), mask_mode=mode, mask_block=blk, k_new=kn.to(gpu),
-                         v_new=vn.to(gpu), **qarg, **args)
+                         v_new=vn.to(gpu), cache_write_kernel=not in_kernel, **qarg, **args)
     as_np = (lambda t: t.cpu().numpy()) if dtype == torch.float16 else (lambda t: t.cpu().view(torch.int16).numpy())
     assert np.array_equal(as_np(kf), exp_k), "K cache differs from the oracle's write"
     assert np.array_equal(as_np(vf), exp_v), "V cache differs from the oracle's write"
