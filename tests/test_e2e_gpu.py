@@ -291,3 +291,31 @@ def test_compiled_forward_surface(gpu):
             if layer == 0:
                 torch.testing.assert_close(a, b, atol=2e-2, rtol=2e-2)
             assert ((a - b).norm() / b.norm()).item() < 1e-2
+
+
+def test_generation_with_confident_model(gpu):
+    """The threshold branch at scale: a 2-layer model whose lm_head is scaled by 30
+    (peaked predictions, so a large share of the masked positions clears p > 0.9 in one
+    step). (1) The HIP generation with the fused sampling step and the same HIP
+    generation with the torch statement of the rule (threshold_unmask) are identical
+    token for token, with several tokens unmasked per row and step (2.1 per row and step,
+    up to 57 of 64 positions in one step, on the seeds below); (2) the eager fp32 oracle,
+    teacher-forced along that trajectory, agrees at >= 95 % of the positions (97.2 %
+    measured), the bar of the 2-layer random-model test."""
+    cfg = _small_cfg()
+    model = em.build_model(cfg, gpu)
+    with torch.no_grad():
+        model.lm_head.weight.mul_(30.0)
+    B, P, N = 8, 64, 128
+    x = _prompts(B, P, cfg.vocab_size, seed=5).to(gpu)
+    fused, st_f = es.generate(model, x, max_new_tokens=N, use_block_cache=True,
+                              impl=es.HipStaticAttention(graphs=True))
+    rec, rule, st_r = _record(model, x, N, True, impl=es.HipStaticAttention(graphs=True))
+    per_row_step = sum(st_f.step_tokens) / (B * len(st_f.step_tokens))
+    print(f"confident model: {len(st_f.step_tokens)} steps, {per_row_step:.2f} tokens per row and step, "
+          f"largest step {max(st_f.step_tokens)} tokens")
+    assert torch.equal(fused, rule), "fused sampling step and the torch rule chose differently"
+    assert per_row_step > 1.5 and max(st_f.step_tokens) > 2 * B, "the threshold branch was hardly taken"
+    rate = _forced_rate(model, x, N, True, rec, rule, EagerStaticAttention())
+    print(f"confident model: teacher-forced agreement with the fp32 oracle {rate:.4f}")
+    assert rate >= 0.95
