@@ -556,7 +556,8 @@ def cpu_baseline_e2e_step(torch):
 
     def run_layer():
         with torch.no_grad():
-            layer(h, pe, cache, False, None, None)
+            hh, m = layer(h, pe, cache, False, None, None)
+            hh + m
 
     def run_head():
         with torch.no_grad():

@@ -113,6 +113,12 @@ SIGNATURES = {
         _c_int, _c_int, _c_int, _c_int,  # B, S, T, H
         _c_int, _c_vp,                  # dtype, stream
     ]),
+    "fdllm_add_rmsnorm": (_c_int, [
+        _c_vp, _c_vp, _c_vp, _c_int,    # x, residual, weight, weight dtype
+        _c_vp, _c_vp, _c_int, _c_int,   # sum out, normed out, rows, hidden size
+        ctypes.c_float, _c_int, _c_int, _c_vp,  # eps, dtype, norm mode, stream
+    ]),
+    "fdllm_silu_mul": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_int, _c_vp]),  # gate, up, out, n, dtype, stream
     "fdllm_kv_attn_workspace_size": (_c_int, [ctypes.POINTER(KVAttnDesc), ctypes.POINTER(_c_sz)]),
     "fdllm_kv_attn_fwd": (_c_int, [ctypes.POINTER(KVAttnDesc), _c_vp, _c_sz, _c_vp]),
     "fdllm_kv_attn_fwd_noalloc": (_c_int, [ctypes.POINTER(KVAttnDesc), _c_vp]),

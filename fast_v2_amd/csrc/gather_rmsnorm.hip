@@ -401,6 +401,119 @@ int launch_gather(const GatherArgs& a, bool vec, hipStream_t stream) {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// ---------------------------------------------------------------------------
+// Residual add + RMSNorm of contiguous rows: the decoder layer's
+//   hidden_states = residual + hidden_states; normed = norm(hidden_states)
+// (modeling.py:465-488 with the norm of :427-432). sum = x + r rounded to the rows' type
+// (as the 16-bit add rounds), written to `sum`; the norm reads that rounded sum. One wave
+// per row, the row in registers (VPL 16-byte vectors per lane), as the gather kernel.
+struct AddNormArgs {
+  const void* x;
+  const void* r;
+  const void* weight;
+  void* sum;
+  void* normed;
+  int rows, H;
+  float eps;
+};
+
+template <typename T, int WK, bool CAST, int VPL>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(const AddNormArgs a) {
+  constexpr int N = Vec16<T>::N;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const int nvec = a.H / N;
+  const u32x4* xr = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.x) + row * a.H);
+  const u32x4* rr = reinterpret_cast<const u32x4*>(static_cast<const T*>(a.r) + row * a.H);
+  u32x4* sr = reinterpret_cast<u32x4*>(static_cast<T*>(a.sum) + row * a.H);
+  u32x4* nr = reinterpret_cast<u32x4*>(static_cast<T*>(a.normed) + row * a.H);
+  // only the last vector can run past the row end (nvec in (64 (VPL - 1), 64 VPL])
+  const int clast = lane + kWave * (VPL - 1);
+  const bool last_in = clast < nvec;
+  u32x4 xv[VPL], rv[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int c = v < VPL - 1 ? lane + kWave * v : (last_in ? clast : nvec - 1);
+    xv[v] = xr[c];
+    rv[v] = rr[c];
+  }
+  float w[VPL][N];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v)
+    load_weight<T, WK, N>(a.weight, (v < VPL - 1 ? lane + kWave * v : (last_in ? clast : nvec - 1)) * N, w[v]);
+  float f[VPL][N];
+  float ss = 0.f;
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    float fx[N], fr[N];
+    Vec16<T>::unpack(xv[v], fx);
+    Vec16<T>::unpack(rv[v], fr);
+    const bool in = v < VPL - 1 || last_in;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      f[v][i] = in ? Vec16<T>::round(fx[i] + fr[i]) : 0.f;
+      ss += f[v][i] * f[v][i];
+    }
+  }
+  ss = wave_allreduce_sum(ss);
+  const float inv = 1.0f / sqrtf(ss / static_cast<float>(a.H) + a.eps);
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    if (v < VPL - 1 || last_in) {
+      const int c = lane + kWave * v;
+      float o[N];
+#pragma unroll
+      for (int i = 0; i < N; ++i) o[i] = apply_norm_ct<T, CAST>(f[v][i], inv, w[v][i]);
+      __builtin_nontemporal_store(Vec16<T>::pack(f[v]), sr + c);
+      __builtin_nontemporal_store(Vec16<T>::pack(o), nr + c);
+    }
+  }
+}
+
+template <typename T, int WK, bool CAST>
+bool launch_add_rmsnorm(const AddNormArgs& a, hipStream_t stream) {
+  const int vpl = (a.H / Vec16<T>::N + kWave - 1) / kWave;
+  const dim3 grid(static_cast<unsigned>((a.rows + 3) / 4));
+  switch (vpl) {
+#define FDLLM_ADD_VPL_CASE(n)                                                          \
+  case n:                                                                              \
+    add_rmsnorm_kernel<T, WK, CAST, n><<<grid, dim3(256), 0, stream>>>(a);             \
+    return true;
+    FDLLM_ADD_VPL_CASE(1)
+    FDLLM_ADD_VPL_CASE(2)
+    FDLLM_ADD_VPL_CASE(3)
+    FDLLM_ADD_VPL_CASE(4)
+    FDLLM_ADD_VPL_CASE(5)
+    FDLLM_ADD_VPL_CASE(6)
+    FDLLM_ADD_VPL_CASE(7)
+    FDLLM_ADD_VPL_CASE(8)
+#undef FDLLM_ADD_VPL_CASE
+    default:
+      return false;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// SiLU-gated product of the MLP, act_fn(gate_proj(x)) * up_proj(x) (modeling.py:164):
+// out = round(round(silu(g)) * u) in the 16-bit type, silu(g) = g / (1 + exp(-g)) in
+// fp32 (the 16-bit SiLU rounds its result, then the product rounds again). Eight
+// elements per thread, 16-byte loads and stores.
+template <typename T>
+__global__ __launch_bounds__(256) void silu_mul_kernel(const u32x4* g, const u32x4* u, u32x4* out, int64_t nvec) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= nvec) return;
+  float fg[8], fu[8], o[8];
+  Vec16<T>::unpack(g[i], fg);
+  Vec16<T>::unpack(u[i], fu);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const float sg = Vec16<T>::round(fg[j] / (1.0f + expf(-fg[j])));
+    o[j] = sg * fu[j];
+  }
+  __builtin_nontemporal_store(Vec16<T>::pack(o), out + i);
+}
+
 }  // namespace
 
 static thread_local char g_last_error[512];
@@ -525,4 +638,72 @@ extern "C" int fdllm_scatter_rows(const void* values, const int64_t* indices, in
   scatter_rows_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
                         static_cast<hipStream_t>(stream)>>>(a);
   FDLLM_RETURN_LAUNCH_STATUS("fdllm_scatter_rows");
+}
+
+extern "C" int fdllm_add_rmsnorm(const void* x, const void* residual, const void* weight, int weight_dtype,
+                                 void* sum_out, void* normed, int rows, int hidden_size, float eps, int dtype,
+                                 int norm_mode, void* stream) {
+  using namespace fdllm;
+  FDLLM_CHECK_ARG(dtype == FDLLM_DTYPE_BF16 || dtype == FDLLM_DTYPE_F16,
+                  "fdllm_add_rmsnorm: dtype %d unsupported (bf16 or fp16)", dtype);
+  FDLLM_CHECK_ARG(norm_mode >= FDLLM_NORM_PLAIN && norm_mode <= FDLLM_NORM_WEIGHT_AFTER_CAST,
+                  "fdllm_add_rmsnorm: unknown norm_mode %d", norm_mode);
+  FDLLM_CHECK_ARG(rows >= 0 && hidden_size > 0 && hidden_size % 8 == 0 && hidden_size <= 8 * 64 * 8,
+                  "fdllm_add_rmsnorm: bad sizes rows=%d H=%d (H a multiple of 8, at most 4096)", rows, hidden_size);
+  if (rows == 0) return FDLLM_OK;
+  FDLLM_CHECK_ARG(x && residual && sum_out && normed, "fdllm_add_rmsnorm: null pointer");
+  FDLLM_CHECK_ARG(aligned16(x) && aligned16(residual) && aligned16(sum_out) && aligned16(normed),
+                  "fdllm_add_rmsnorm: rows must be 16-byte aligned");
+  FDLLM_CHECK_ARG(norm_mode == FDLLM_NORM_PLAIN || weight != nullptr, "fdllm_add_rmsnorm: norm_mode %d needs a weight",
+                  norm_mode);
+  FDLLM_CHECK_ARG(norm_mode == FDLLM_NORM_PLAIN || weight_dtype == FDLLM_DTYPE_F32 || weight_dtype == dtype,
+                  "fdllm_add_rmsnorm: weight dtype %d must be fp32 or the rows' type", weight_dtype);
+  FDLLM_CHECK_ARG(norm_mode == FDLLM_NORM_PLAIN || aligned16(weight), "fdllm_add_rmsnorm: weight must be 16-byte aligned");
+  FDLLM_CHECK_ARG(!(eps < 0.f), "fdllm_add_rmsnorm: eps must be >= 0");
+  AddNormArgs a;
+  a.x = x;
+  a.r = residual;
+  a.weight = weight;
+  a.sum = sum_out;
+  a.normed = normed;
+  a.rows = rows;
+  a.H = hidden_size;
+  a.eps = eps;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool cast = norm_mode == FDLLM_NORM_WEIGHT_AFTER_CAST;
+  bool done;
+  if (dtype == FDLLM_DTYPE_BF16) {
+    if (norm_mode == FDLLM_NORM_PLAIN) done = launch_add_rmsnorm<bf16_t, kWNone, false>(a, s);
+    else if (weight_dtype == FDLLM_DTYPE_F32)
+      done = cast ? launch_add_rmsnorm<bf16_t, kW32, true>(a, s) : launch_add_rmsnorm<bf16_t, kW32, false>(a, s);
+    else done = cast ? launch_add_rmsnorm<bf16_t, kW16, true>(a, s) : launch_add_rmsnorm<bf16_t, kW16, false>(a, s);
+  } else {
+    if (norm_mode == FDLLM_NORM_PLAIN) done = launch_add_rmsnorm<f16_t, kWNone, false>(a, s);
+    else if (weight_dtype == FDLLM_DTYPE_F32)
+      done = cast ? launch_add_rmsnorm<f16_t, kW32, true>(a, s) : launch_add_rmsnorm<f16_t, kW32, false>(a, s);
+    else done = cast ? launch_add_rmsnorm<f16_t, kW16, true>(a, s) : launch_add_rmsnorm<f16_t, kW16, false>(a, s);
+  }
+  FDLLM_CHECK_ARG(done, "fdllm_add_rmsnorm: hidden_size %d unsupported", hidden_size);
+  FDLLM_RETURN_LAUNCH_STATUS("fdllm_add_rmsnorm");
+}
+
+extern "C" int fdllm_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream) {
+  using namespace fdllm;
+  FDLLM_CHECK_ARG(dtype == FDLLM_DTYPE_BF16 || dtype == FDLLM_DTYPE_F16,
+                  "fdllm_silu_mul: dtype %d unsupported (bf16 or fp16)", dtype);
+  FDLLM_CHECK_ARG(n >= 0 && n % 8 == 0, "fdllm_silu_mul: n = %lld must be a multiple of 8", static_cast<long long>(n));
+  if (n == 0) return FDLLM_OK;
+  FDLLM_CHECK_ARG(gate && up && out, "fdllm_silu_mul: null pointer");
+  FDLLM_CHECK_ARG(aligned16(gate) && aligned16(up) && aligned16(out), "fdllm_silu_mul: tensors must be 16-byte aligned");
+  const int64_t nvec = n / 8;
+  FDLLM_CHECK_ARG(nvec / 256 < (int64_t{1} << 31), "fdllm_silu_mul: n too large");
+  const dim3 grid(static_cast<unsigned>((nvec + 255) / 256));
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == FDLLM_DTYPE_BF16)
+    silu_mul_kernel<bf16_t><<<grid, dim3(256), 0, s>>>(static_cast<const u32x4*>(gate), static_cast<const u32x4*>(up),
+                                                       static_cast<u32x4*>(out), nvec);
+  else
+    silu_mul_kernel<f16_t><<<grid, dim3(256), 0, s>>>(static_cast<const u32x4*>(gate), static_cast<const u32x4*>(up),
+                                                      static_cast<u32x4*>(out), nvec);
+  FDLLM_RETURN_LAUNCH_STATUS("fdllm_silu_mul");
 }

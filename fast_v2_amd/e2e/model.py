@@ -84,11 +84,25 @@ class RMSNorm(nn.Module):
         h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + self.variance_epsilon)
         return self.weight * h.to(dt)
 
+    def add_norm(self, h: torch.Tensor, a: torch.Tensor):
+        """(h + a, norm(h + a)): the residual add that precedes the norm in the decoder
+        layer (modeling.py:475-484). Fused, one kernel reads h and a once and writes the
+        rounded sum and its norm; the sum is the 16-bit add's, bit for bit, and the norm
+        that of ``forward`` on it."""
+        if self.fused:
+            from .. import _ffi, ops
+            return ops.add_rmsnorm(h, a, self.weight, self.variance_epsilon, _ffi.NORM_WEIGHT_AFTER_CAST)
+        s = h + a
+        return s, self(s)
+
 
 def set_fused_norms(model: nn.Module, on: bool) -> None:
-    """Switch every RMSNorm of ``model`` to the fused kernel (or back to torch)."""
+    """Switch every RMSNorm of ``model`` to the fused kernels, and the MLPs' SiLU-gated
+    product to its kernel (or both back to torch)."""
     for mod in model.modules():
         if isinstance(mod, RMSNorm):
+            mod.fused = on
+        elif isinstance(mod, MLP):
             mod.fused = on
 
 
@@ -114,8 +128,12 @@ class MLP(nn.Module):
         self.gate_proj = nn.Linear(cfg.hidden_size, cfg.intermediate_size, bias=False)
         self.up_proj = nn.Linear(cfg.hidden_size, cfg.intermediate_size, bias=False)
         self.down_proj = nn.Linear(cfg.intermediate_size, cfg.hidden_size, bias=False)
+        self.fused = False
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if self.fused:
+            from .. import ops
+            return self.down_proj(ops.silu_mul(self.gate_proj(x), self.up_proj(x)))
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
 
@@ -128,11 +146,20 @@ class DecoderLayer(nn.Module):
         self.post_attention_layernorm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps)
 
     def forward(self, h, position_embeddings, past_key_value, update_past_key_values, block_past_key_values,
-                replace_position):
-        a = self.self_attn(self.input_layernorm(h), position_embeddings, None, past_key_value, None,
+                replace_position, pending: Optional[torch.Tensor] = None):
+        """Returns (h, m) with the layer's output h + m (modeling.py:465-488). The MLP's
+        residual add is left to the caller so that it runs together with the next norm
+        (the next layer's input norm, or the final norm); ``pending`` is the previous
+        layer's m, added to h before this layer's input norm. The sums are the same 16-bit
+        adds as ``h = residual + h`` in the reference layer, in the same order."""
+        if pending is None:
+            x = self.input_layernorm(h)
+        else:
+            h, x = self.input_layernorm.add_norm(h, pending)
+        a = self.self_attn(x, position_embeddings, None, past_key_value, None,
                            update_past_key_values, block_past_key_values, replace_position)
-        h = h + a
-        return h + self.mlp(self.post_attention_layernorm(h))
+        h, x = self.post_attention_layernorm.add_norm(h, a)
+        return h, self.mlp(x)
 
 
 class Backbone(nn.Module):
@@ -202,9 +229,10 @@ class BlockDiffusionLM(nn.Module):
             cache_position = torch.arange(start, start + S, device=input_ids.device)
         pe = self.model.rotary(cache_position, h.dtype)
         bpkv = block_past_key_values if use_block_cache else None
+        m = None
         for layer in self.model.layers:
-            h = layer(h, pe, past_key_values, update_past_key_values, bpkv, replace_position)
-        h = self.model.norm(h)
+            h, m = layer(h, pe, past_key_values, update_past_key_values, bpkv, replace_position, m)
+        h = self.model.norm(h) if m is None else self.model.norm.add_norm(h, m)[1]
         if logits_to_keep:
             h = h[:, -logits_to_keep:]
         return self.lm_head(h)

@@ -133,6 +133,51 @@ def gather_rmsnorm(
     return normed, gathered
 
 
+def add_rmsnorm(x: torch.Tensor, residual: torch.Tensor, weight: Optional[torch.Tensor], eps: float,
+                norm_mode: int = _ffi.NORM_WEIGHT_AFTER_CAST) -> Tuple[torch.Tensor, torch.Tensor]:
+    """``s = x + residual`` (rounded to the rows' dtype) and the RMSNorm of ``s`` in one
+    pass over the rows (modeling.py:465-488, 427-432). x, residual [..., H] bf16 / fp16 of
+    one shape, H a multiple of 8 (at most 4096). Returns (s, normed), both new tensors."""
+    if x.shape != residual.shape or x.dtype != residual.dtype:
+        raise RuntimeError("add_rmsnorm: x and residual must share shape and dtype")
+    dev = _require_gpu(x, residual, *([weight] if weight is not None else []))
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError("add_rmsnorm: dtype must be bf16 or fp16")
+    H = x.shape[-1]
+    x, residual = x.contiguous(), residual.contiguous()
+    if weight is not None:
+        weight = weight.contiguous()
+        if weight.numel() != H:
+            raise RuntimeError("add_rmsnorm: weight size must equal hidden size")
+    elif norm_mode != _ffi.NORM_PLAIN:
+        raise RuntimeError("add_rmsnorm: this norm_mode needs a weight")
+    out_sum = torch.empty_like(x)
+    normed = torch.empty_like(x)
+    rc = _ffi.lib().fdllm_add_rmsnorm(
+        x.data_ptr(), residual.data_ptr(), _ptr(weight), _ffi.dtype_code(weight.dtype) if weight is not None else 0,
+        out_sum.data_ptr(), normed.data_ptr(), x.numel() // H, H, float(eps), _ffi.dtype_code(x.dtype),
+        int(norm_mode), _ffi.stream_ptr(dev))
+    _ffi.check(rc, "fdllm_add_rmsnorm")
+    return out_sum, normed
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """``silu(gate) * up`` in the 16-bit dtype with torch's rounding points (the SiLU's
+    result rounded, then the product): the MLP's act_fn(gate_proj(x)) * up_proj(x)
+    (modeling.py:164). gate, up of one shape, bf16 / fp16, numel a multiple of 8."""
+    if gate.shape != up.shape or gate.dtype != up.dtype:
+        raise RuntimeError("silu_mul: gate and up must share shape and dtype")
+    dev = _require_gpu(gate, up)
+    if gate.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError("silu_mul: dtype must be bf16 or fp16")
+    gate, up = gate.contiguous(), up.contiguous()
+    out = torch.empty_like(gate)
+    rc = _ffi.lib().fdllm_silu_mul(gate.data_ptr(), up.data_ptr(), out.data_ptr(), gate.numel(),
+                                   _ffi.dtype_code(gate.dtype), _ffi.stream_ptr(dev))
+    _ffi.check(rc, "fdllm_silu_mul")
+    return out
+
+
 def scatter_rows(values: torch.Tensor, indices: torch.Tensor,
                  cache: torch.Tensor, current: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
     """cache[b, indices[b,t]] = values[b, t] (and current[b, indices[b,t]] when given).

@@ -119,6 +119,34 @@ int fdllm_scatter_rows(const void* values, const int64_t* indices, int64_t indic
                        int dtype, void* stream);
 
 /* -------------------------------------------------------------------------
+ * Residual add + RMSNorm of contiguous rows (the decoder layer around the path):
+ *
+ *   sum[r, :]    = to_dtype(x[r, :] + residual[r, :])
+ *   normed[r, :] = the norm of sum[r, :] in `norm_mode` (as fdllm_gather_rmsnorm)
+ *
+ * x, residual, sum_out, normed: [rows, hidden_size] in `dtype` (bf16 or fp16),
+ * contiguous and 16-byte aligned; hidden_size a multiple of 8, at most 4096; the
+ * weight in fp32 or `dtype`.
+ *
+ * Replaces: hidden_states = residual + hidden_states followed by the next RMSNorm
+ * (modeling.py:465-488, 427-432 of the Fast_dLLM_v2_7B snapshot).
+ * ------------------------------------------------------------------------- */
+int fdllm_add_rmsnorm(const void* x, const void* residual, const void* weight, int weight_dtype,
+                      void* sum_out, void* normed, int rows, int hidden_size, float eps, int dtype,
+                      int norm_mode, void* stream);
+
+/* -------------------------------------------------------------------------
+ * SiLU-gated product of the MLP:
+ *
+ *   out[i] = to_dtype(to_dtype(silu(gate[i])) * up[i]),  silu(g) = g / (1 + exp(-g)) in fp32
+ *
+ * gate, up, out: n elements of `dtype` (bf16 or fp16), n a multiple of 8, 16-byte aligned.
+ *
+ * Replaces: act_fn(gate_proj(x)) * up_proj(x) (modeling.py:164 of the snapshot).
+ * ------------------------------------------------------------------------- */
+int fdllm_silu_mul(const void* gate, const void* up, void* out, int64_t n, int dtype, void* stream);
+
+/* -------------------------------------------------------------------------
  * Block attention over a (paged) KV cache.
  *
  * Query row (b, i, h) attends to the keys j of sequence b that the mask allows,

@@ -130,6 +130,14 @@ def test_rejected_arguments_launch_nothing(lib):
     r.head_dim = 128  # no tensors given
     assert lib.fdllm_rope_kv_write(ctypes.byref(r), None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
     assert b"null" in lib.fdllm_last_error()
+    # residual add + norm: hidden size not a multiple of 8; SiLU product: ragged length
+    rc = lib.fdllm_add_rmsnorm(None, None, None, 0, None, None, 4, 100, 1e-6, _ffi.DTYPE_BF16, _ffi.NORM_PLAIN, None)
+    assert rc == _ffi.FDLLM_ERR_INVALID_ARGUMENT and b"multiple of 8" in lib.fdllm_last_error()
+    rc = lib.fdllm_add_rmsnorm(None, None, None, 0, None, None, 4, 64, 1e-6, _ffi.DTYPE_F32, _ffi.NORM_PLAIN, None)
+    assert rc == _ffi.FDLLM_ERR_INVALID_ARGUMENT and b"dtype" in lib.fdllm_last_error()
+    assert lib.fdllm_silu_mul(None, None, None, 12, _ffi.DTYPE_BF16, None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    assert lib.fdllm_silu_mul(None, None, None, 16, _ffi.DTYPE_BF16, None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    assert b"null" in lib.fdllm_last_error()
 
 
 def test_workspace_size_for_the_decode_workload(lib):

@@ -222,3 +222,83 @@ def test_scatter_rows(gpu):
     ret = ops.scatter_rows(vals.to(gpu), idx.to(gpu), c_gpu, u_gpu)
     assert ret.data_ptr() == u_gpu.data_ptr()
     assert torch.equal(c_gpu.cpu(), exp_cache) and torch.equal(u_gpu.cpu(), exp_cur)
+
+
+@pytest.mark.parametrize("rows,H,dtype", [
+    (128, 3584, torch.bfloat16),   # the 7B sub-block step: 16 sequences x 8 tokens
+    (2048, 3584, torch.bfloat16),  # a 4 x 512-token prompt
+    (37, 2056, torch.bfloat16),    # 257 vectors: the last one per lane ragged
+    (5, 4096, torch.float16),
+    (3, 8, torch.bfloat16),
+])
+def test_add_rmsnorm(gpu, rows, H, dtype):
+    """The decoder layer's residual add + norm: the sum bit-exact against the 16-bit torch
+    add, the norm bit-exact against the gather kernel on that sum (the norm the model used
+    before the add was fused) and within the gather bars of the oracle."""
+    print(f"case add_rmsnorm rows={rows} H={H} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(rows + H)
+    x = (2 * torch.randn(rows, H, generator=g)).to(dtype)
+    r = (2 * torch.randn(rows, H, generator=g)).to(dtype)
+    w = (1 + 0.05 * torch.randn(H, generator=g)).to(dtype)
+    s_exp = x + r
+    for wt in (w, w.float()):
+        s, n = ops.add_rmsnorm(x.to(gpu), r.to(gpu), wt.to(gpu), 1e-6)
+        assert torch.equal(s.cpu(), s_exp)
+        idx = torch.arange(rows, dtype=torch.int64, device=gpu)[None]
+        n_gather, _ = ops.gather_rmsnorm(s[None], idx, wt.to(gpu), 1e-6, og.NORM_WEIGHT_AFTER_CAST, False)
+        assert torch.equal(n.cpu(), n_gather[0].cpu())
+        tag = "bf16" if dtype == torch.bfloat16 else "f16"
+        _, exp_n = og.gather_rmsnorm_np(s_exp.float().numpy()[None], np.arange(rows)[None], wt.float().numpy(), 1e-6,
+                                        og.NORM_WEIGHT_AFTER_CAST, tag)
+        np.testing.assert_allclose(n.float().cpu().numpy(), exp_n[0], atol=ATOL, rtol=RTOL)
+        if dtype == torch.bfloat16:
+            assert _ulp_diff_bf16(n.cpu(), torch.from_numpy(exp_n[0]).to(torch.bfloat16)) <= 2
+    # plain mode (no weight) and the torch statement of the model norm
+    s, n = ops.add_rmsnorm(x.to(gpu), r.to(gpu), None, 1e-6, og.NORM_PLAIN)
+    _, exp_n = og.gather_rmsnorm_np(s_exp.float().numpy()[None], np.arange(rows)[None], None, 1e-6, og.NORM_PLAIN,
+                                    "bf16" if dtype == torch.bfloat16 else "f16")
+    np.testing.assert_allclose(n.float().cpu().numpy(), exp_n[0], atol=ATOL, rtol=RTOL)
+
+
+def test_add_rmsnorm_errors(gpu):
+    x = torch.randn(4, 100, device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="hidden_size|H="):
+        ops.add_rmsnorm(x, x.clone(), torch.ones(100, device=gpu), 1e-6)  # H not a multiple of 8
+    y = torch.randn(4, 64, device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError):
+        ops.add_rmsnorm(y, y.half(), torch.ones(64, device=gpu), 1e-6)
+    s, n = ops.add_rmsnorm(y[:0], y[:0], torch.ones(64, device=gpu), 1e-6)
+    assert s.shape == (0, 64) and n.shape == (0, 64)
+
+
+@pytest.mark.parametrize("shape,dtype", [
+    ((128, 18944), torch.bfloat16),   # the 7B MLP at the sub-block step
+    ((3, 77, 24), torch.bfloat16),
+    ((1024, 512), torch.float16),
+])
+def test_silu_mul(gpu, shape, dtype):
+    """silu(gate) * up: bit-exact against the torch statement on the GPU (SiLU in fp32,
+    rounded, then the 16-bit product), within one ulp of a float64 restatement."""
+    print(f"case silu_mul {shape} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(sum(shape))
+    gate = (4 * torch.randn(*shape, generator=g)).to(dtype)
+    up = torch.randn(*shape, generator=g).to(dtype)
+    gate[..., :4] = torch.tensor([0.0, -0.0, 30.0, -30.0])   # zeros and saturated ends
+    got = ops.silu_mul(gate.to(gpu), up.to(gpu))
+    exp = torch.nn.functional.silu(gate.to(gpu)) * up.to(gpu)
+    assert torch.equal(got.cpu(), exp.cpu())
+    g64 = gate.double()
+    sg = (g64 / (1 + torch.exp(-g64))).to(dtype).double()
+    ref = (sg * up.double()).to(dtype)
+    if dtype == torch.bfloat16:
+        assert _ulp_diff_bf16(got.cpu(), ref) <= 1
+    else:
+        torch.testing.assert_close(got.cpu(), ref, atol=1e-3, rtol=1e-3)
+
+
+def test_silu_mul_errors(gpu):
+    a = torch.randn(7, device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="multiple of 8"):
+        ops.silu_mul(a, a.clone())
+    with pytest.raises(RuntimeError):
+        ops.silu_mul(torch.randn(8, device=gpu), torch.randn(8, device=gpu))
