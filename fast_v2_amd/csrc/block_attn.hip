@@ -35,6 +35,7 @@
 //     splits' loads in flight). The kernel boundary orders the two, so no
 //     device-scope fence or counter is needed.
 #include <algorithm>
+#include <climits>
 #include <mutex>
 
 #include "fdllm_common.h"
@@ -2146,7 +2147,13 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
   u32x4 qf[8];  // loaded after the first tiles are issued (see the main loop)
   const int lim_min =
       __builtin_amdgcn_readfirstlane(-static_cast<int>(wave_allreduce_max(-static_cast<float>(lim))));
-  const int lim_max = __builtin_amdgcn_readfirstlane(static_cast<int>(wave_allreduce_max(static_cast<float>(lim))));
+  // A wave whose 32 rows are all padding (past the unit's R rows: the full block's 224
+  // rows fill 7 of the 8 waves) issues its share of the tile loads and passes every
+  // barrier, but computes nothing: no tile is active for it (kb < INT_MIN never holds).
+  const int lim_max =
+      row0 + __builtin_amdgcn_readfirstlane(wave) * 32 >= p.R
+          ? INT_MIN
+          : __builtin_amdgcn_readfirstlane(static_cast<int>(wave_allreduce_max(static_cast<float>(lim))));
   const float c2 = p.scale_log2;
   const float rescale_thr = 8.f / c2;
 
