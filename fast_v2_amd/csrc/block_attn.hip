@@ -2023,6 +2023,24 @@ __device__ __forceinline__ i32x4 make_srd(const void* base, int bytes) {
 #ifndef FDLLM_PREFILL_PIPE
 #define FDLLM_PREFILL_PIPE 1
 #endif
+// LDS operand reads issued ahead of their MFMA in the ring kernel's ping-pong phases:
+// K fragments of S = K Q^T, and the V^T fragment pairs of O^T += V^T P^T (0 leaves the
+// PV order to the compiler, which kept one to two MFMAs of reads in flight). Measured on
+// one box (4 x 4096 prefill with the cache write / bs16 full-block step): PV 0 465.0 /
+// 45.56 us, PV 4 459.6 / 45.19 us; PV 2, 6, 8 within 0.3 % of PV 4 or slower; QK 8
+// instead of 4 no faster (465.9 / 45.75 us).
+#ifndef FDLLM_QK_READ_AHEAD
+#define FDLLM_QK_READ_AHEAD 4
+#endif
+// 1: the ring kernel sums a tile's probabilities in four partial sums instead of one
+// chain. Measured and not kept: 465.9 -> 464.1 us / 46.81 -> 46.58 us on one box, within
+// the spread between boxes, and it changes the sums' rounding.
+#ifndef FDLLM_RING_LSUM_TREE
+#define FDLLM_RING_LSUM_TREE 0
+#endif
+#ifndef FDLLM_PV_READ_AHEAD
+#define FDLLM_PV_READ_AHEAD 4
+#endif
 // Key halves (32 keys) whose page ids the ring prefill kernel stages in LDS: 65536 keys
 // per workgroup; longer paged ranges take kv_prefill_kernel.
 constexpr int kRingMaxHalves = 2048;
@@ -2391,13 +2409,14 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
     for (int ks = 0; ks < 8; ++ks)
 #pragma unroll
       for (int st = 0; st < 2; ++st) s[st] = mfma32x32x16<F16>(kf[ks][st], qf[ks], s[st]);
-    __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS reads
+    constexpr int RA = FDLLM_QK_READ_AHEAD;
+    __builtin_amdgcn_sched_group_barrier(0x100, RA, 0);  // DS reads
 #pragma unroll
-    for (int i = 0; i < 12; ++i) {
+    for (int i = 0; i < 16 - RA; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+    __builtin_amdgcn_sched_group_barrier(0x008, RA, 0);
   };
   auto pv = [&](const u32x4 (&P)[4], int slot) __attribute__((always_inline)) {
     const uint8_t* sv = ring + slot * TB;
@@ -2411,6 +2430,16 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
                                                        sv + kk * 4096 + 2048 + vaddr[dt])));
         acc[dt] = mfma32x32x16<F16>(u32x4{lo[0], lo[1], hi[0], hi[1]}, P[kk], acc[dt]);
       }
+    if constexpr (FDLLM_PV_READ_AHEAD > 0) {
+      constexpr int RA = FDLLM_PV_READ_AHEAD;  // MFMAs whose two reads go ahead
+      __builtin_amdgcn_sched_group_barrier(0x100, 2 * RA, 0);
+#pragma unroll
+      for (int i = 0; i < 16 - RA; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, RA, 0);
+    }
   };
   // softmax of the scores s of the tile at keys kb: mask, running max (lazy rescale of
   // acc), exponentials, running sum; P = the probabilities packed as the PV operand
@@ -2439,6 +2468,18 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
       m_run = m_new;
     }
     const float mc = m_run == -INFINITY ? 0.f : m_run * c2;
+#if FDLLM_RING_LSUM_TREE
+    float ls[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const float v = fast_exp2(fmaf(s[st][e], c2, -mc));
+        s[st][e] = v;
+        ls[e & 3] += v;
+      }
+    l_run += (ls[0] + ls[1]) + (ls[2] + ls[3]);
+#else
     float lsum = 0.f;
 #pragma unroll
     for (int st = 0; st < 2; ++st)
@@ -2449,6 +2490,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
         lsum += v;
       }
     l_run += lsum;
+#endif
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const int st = kk >> 1;
