@@ -411,8 +411,16 @@ def bench_e2e(torch, args):
     _log("e2e: timed generation")
     out, st = es.generate(model, x, max_new_tokens=args.e2e_tokens, use_block_cache=True,
                           progress=lambda st_: progress(st_, "timed run"))
+    # the same generation with the q / k / v projections in the RoPE + cache-write kernel
+    # (off by default: its projections differ from the library GEMM's in the last bit)
+    _log("e2e: timed generation with the fused q / k / v projections")
+    out_f, st_f = es.generate(model, x, max_new_tokens=args.e2e_tokens, use_block_cache=True,
+                              impl=es.HipStaticAttention(fused_qkv=True),
+                              progress=lambda st_: progress(st_, "timed run, fused projections"))
     tun.enable(False)
-    res = {"tokens_per_s": round(st.tokens_per_second, 1), "generated_tokens": st.generated_tokens,
+    res = {"tokens_per_s": round(st.tokens_per_second, 1),
+           "tokens_per_s_fused_qkv_projection": round(st_f.tokens_per_second, 1),
+           "generated_tokens": st.generated_tokens,
            "seconds": round(st.seconds, 3), "forwards": st.forwards, "commits": st.commits,
            "ms_per_forward": round(st.seconds * 1e3 / max(st.forwards, 1), 3),
            "tokens_per_step": round(sum(st.step_tokens) / max(len(st.step_tokens), 1), 3),
@@ -425,7 +433,7 @@ def bench_e2e(torch, args):
                                            "block never completes"),
            "config": "28 layers, hidden 3584, 28/4 heads, vocab 152064, bf16; batch 16, prompt 512, "
                      f"{args.e2e_tokens} new tokens, block 32, sub-block 8, threshold 0.9 (p > 0.9), block cache on"}
-    del model, out, x
+    del model, out, out_f, x
     torch.cuda.empty_cache()
     return res
 

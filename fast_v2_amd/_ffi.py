@@ -94,6 +94,15 @@ class RopeKVDesc(ctypes.Structure):
     ]
 
 
+class QkvRopeDesc(ctypes.Structure):
+    """Mirror of ``fdllm_qkv_rope_desc`` (include/fdllm_hip.h)."""
+
+    _fields_ = [
+        ("x", _c_vp), ("x_stride_row", _c_i64), ("wq", _c_vp), ("wk", _c_vp), ("wv", _c_vp),
+        ("bq", _c_vp), ("bk", _c_vp), ("bv", _c_vp), ("hidden", _c_i32), ("rope", RopeKVDesc),
+    ]
+
+
 # name -> (restype, argtypes); every symbol of include/fdllm_hip.h
 SIGNATURES = {
     "fdllm_abi_version": (_c_int, []),
@@ -131,6 +140,7 @@ SIGNATURES = {
         _c_int, _c_vp,                          # dtype, stream
     ]),
     "fdllm_rope_kv_write": (_c_int, [ctypes.POINTER(RopeKVDesc), _c_vp]),
+    "fdllm_qkv_rope_kv_write": (_c_int, [ctypes.POINTER(QkvRopeDesc), _c_vp]),
     "fdllm_unmask_step": (_c_int, [
         _c_vp, _c_i64, _c_i64, _c_int,          # logits, batch stride, row stride, vocab
         _c_int, _c_int,                         # row_offset, shift

@@ -44,7 +44,6 @@ namespace fdllm {
 namespace {
 
 constexpr int kKT = 64;        // keys per tile
-constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 (gfx9: 32-bit data format)
 constexpr int kThreads = 256;  // 4 waves
 constexpr int kSlcNt = 2;      // buffer-load cache policy: streaming (no reuse expected)
 // Buffer load/store cache policy "sc1": coherent at device scope. With 8 XCDs the L2
@@ -161,14 +160,6 @@ typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
 // ds_read_b64_tr_b16: transposing LDS read of four 16-bit values (see kv_decode_kernel).
 __device__ __forceinline__ s16x4 lds_read_tr16(const uint16_t* lds_ptr) {
   return __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(lds_ptr));
-}
-
-// Workgroup barrier that orders LDS only: waits for this wave's LDS operations,
-// then s_barrier. Outstanding global loads stay in flight across it.
-__device__ __forceinline__ void lds_barrier() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 }
 
 // Exclusive key bound for query token t of sequence b.
@@ -1365,7 +1356,6 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   FDLLM_STAMP(5, __builtin_amdgcn_s_memrealtime());  // merge written (last arrival)
 }
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 // max / sum of the values of lanes l and l ^ 32 (v_permlane32_swap_b32: both
 // results hold lanes 0-31 of one operand and lanes 32-63 of the other, so each
@@ -1377,17 +1367,6 @@ __device__ __forceinline__ float halves_max(float v) {
 __device__ __forceinline__ float halves_sum(float v) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
-template <bool F16>
-__device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
-  if constexpr (F16) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
-                                                  0);
-  } else {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
-                                                   0, 0);
-  }
 }
 
 // fp32 attention: fp32 inputs, fp32 output, fp32 arithmetic throughout (the reference's
@@ -2004,19 +1983,6 @@ __global__ __launch_bounds__(64 * NW, 2) void kv_prefill_kernel(FDLLM_LEAD_PARAM
   }
 }
 
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-
-// Raw buffer descriptor in scalar registers: base address, size in bytes, 32-bit format.
-__device__ __forceinline__ i32x4 make_srd(const void* base, int bytes) {
-  const uint64_t a = reinterpret_cast<uint64_t>(base);
-  i32x4 r;
-  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
-  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32));
-  r[2] = __builtin_amdgcn_readfirstlane(bytes);
-  r[3] = kBufferFlags;
-  return r;
-}
-
 // 1: the ping-pong schedule below (two tiles in flight); 0: the plain schedule (three
 // tiles in flight, every wave runs S, softmax, PV in turn). On the 4 x 4096-token
 // prefill the ping-pong form measured 475-482 us against 484-488 us for the plain one.
@@ -2044,36 +2010,6 @@ __device__ __forceinline__ i32x4 make_srd(const void* base, int bytes) {
 // Key halves (32 keys) whose page ids the ring prefill kernel stages in LDS: 65536 keys
 // per workgroup; longer paged ranges take kv_prefill_kernel.
 constexpr int kRingMaxHalves = 2048;
-
-// Direct-to-LDS load: 16 bytes per lane from buffer offset voff to LDS byte address
-// lds + 16 * lane (one 1 KB block per wave; lanes past the descriptor's size write
-// zeros without memory traffic). The compiler does not see the LDS write, so readers
-// wait with wait_vmcnt and a barrier; M0 is restored after the load.
-__device__ __forceinline__ void lds_dma16(i32x4 srd_in, int voff, uint32_t lds_in) {
-  // both are wave-uniform by construction; readfirstlane puts them in scalar registers
-  i32x4 srd;
-#pragma unroll
-  for (int i = 0; i < 4; ++i) srd[i] = __builtin_amdgcn_readfirstlane(srd_in[i]);
-  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_in);
-  int saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(voff), "s"(srd), "s"(lds));
-}
-
-// Wait until at most N vector memory operations of this wave are outstanding.
-// Neither asm declares a memory clobber: such a clobber would keep every local whose
-// address a lambda captured in scratch memory. Their order against the LDS reads comes
-// from the workgroup barrier between them (volatile asm is not moved across the
-// barrier and its fences).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
-}
 
 // ---------------------------------------------------------------------------
 // Prefill attention with direct-to-LDS staging (same work split, math and results

@@ -118,6 +118,76 @@ __device__ __forceinline__ float group4_allreduce_sum(float v) {
   return v;
 }
 
+// ---------------------------------------------------------------------------
+// MFMA, buffer descriptors and direct-to-LDS staging shared by the attention and
+// projection kernels.
+// ---------------------------------------------------------------------------
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kBufferFlags = 0x00020000;  // raw buffer descriptor word 3 (gfx9: 32-bit data format)
+
+template <bool F16>
+__device__ __forceinline__ f32x16 mfma32x32x16(const u32x4& a, const u32x4& b, const f32x16& c) {
+  if constexpr (F16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                  0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                   0, 0);
+  }
+}
+
+// Raw buffer descriptor in scalar registers: base address, size in bytes, 32-bit format.
+__device__ __forceinline__ i32x4 make_srd(const void* base, int bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane(static_cast<int>(a & 0xffffffffu));
+  r[1] = __builtin_amdgcn_readfirstlane(static_cast<int>(a >> 32));
+  r[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r[3] = kBufferFlags;
+  return r;
+}
+
+// Direct-to-LDS load: 16 bytes per lane from buffer offset voff to LDS byte address
+// lds + 16 * lane (one 1 KB block per wave; lanes past the descriptor's size write
+// zeros without memory traffic). The compiler does not see the LDS write, so readers
+// wait with wait_vmcnt and a barrier; M0 is restored after the load.
+__device__ __forceinline__ void lds_dma16(i32x4 srd_in, int voff, uint32_t lds_in) {
+  // both are wave-uniform by construction; readfirstlane puts them in scalar registers
+  i32x4 srd;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) srd[i] = __builtin_amdgcn_readfirstlane(srd_in[i]);
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_in);
+  int saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voff), "s"(srd), "s"(lds));
+}
+
+// Wait until at most N vector memory operations of this wave are outstanding.
+// Neither asm declares a memory clobber: such a clobber would keep every local whose
+// address a lambda captured in scratch memory. Their order against the LDS reads comes
+// from the workgroup barrier between them (volatile asm is not moved across the
+// barrier and its fences).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N));
+}
+
+// Workgroup barrier that orders LDS only: waits for this wave's LDS operations,
+// then s_barrier. Outstanding global loads stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+
 }  // namespace fdllm
 
 // ---------------------------------------------------------------------------

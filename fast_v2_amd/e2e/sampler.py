@@ -30,6 +30,7 @@ from typing import Optional
 import torch
 
 from .. import ops
+from ..utils import attention_backends as ab
 from ..utils.attention_backends import get_attention_backend, patch_attention_layers, unpatch_attention_layers
 from ..utils.static_kv_cache import StaticBlockCache, StaticKVCache
 from .model import set_fused_norms
@@ -42,10 +43,14 @@ class HipStaticAttention:
 
     name = "hip"
 
-    def __init__(self, graphs: bool = True, fused_norm: bool = True, fused_sampler: bool = True):
+    def __init__(self, graphs: bool = True, fused_norm: bool = True, fused_sampler: bool = True,
+                 fused_qkv: bool = False):
         self.graphs = graphs
         self.fused_norm = fused_norm
         self.fused_sampler = fused_sampler
+        # the q / k / v projections in the RoPE + cache-write kernel (attention_backends.FUSED_QKV_PROJECTION)
+        self.fused_qkv = fused_qkv
+        self._saved_qkv = None
 
     def make_caches(self, batch, max_seq_len, cfg, dtype, device, use_block_cache):
         cache = StaticKVCache(batch, max_seq_len, cfg.num_hidden_layers, cfg.num_key_value_heads, cfg.head_dim,
@@ -57,11 +62,15 @@ class HipStaticAttention:
     def patch(self, model, block_cache):
         if self.fused_norm:
             set_fused_norms(model, True)
+        self._saved_qkv = ab.FUSED_QKV_PROJECTION
+        ab.FUSED_QKV_PROJECTION = self.fused_qkv
         return patch_attention_layers(model, get_attention_backend("hip"), block_cache)
 
     def unpatch(self, model, originals):
         unpatch_attention_layers(model, originals)
         set_fused_norms(model, False)
+        if self._saved_qkv is not None:
+            ab.FUSED_QKV_PROJECTION = self._saved_qkv
 
 
 class ForwardGraphs:

@@ -359,6 +359,66 @@ def block_attn(
     return out
 
 
+def _rope_dest_desc(d, B, S, Hq, Hkv, D, dtype, dev, cos, sin, k_cache, v_cache, write_start, write_offset,
+                    k_block, v_block, block_offset, q_out, kv_out):
+    """Validate the RoPE / cache-write arguments shared by rope_kv_write and
+    qkv_rope_kv_write and fill those fields of ``d`` (a RopeKVDesc); returns
+    (q_out, (k_out, v_out) or (None, None), keep): ``keep`` holds the tensors the
+    descriptor points to that this function made, for the caller to hold until the
+    launch."""
+    if cos.dim() == 2:
+        cos, sin = cos[None], sin[None]
+    if cos.shape != sin.shape or cos.dim() != 3 or cos.shape[1] != S or cos.shape[2] != D or \
+            cos.shape[0] not in (1, B):
+        raise RuntimeError("rope_kv_write: cos / sin must be [1 or B, S, D]")
+    if (k_cache is None) != (v_cache is None) or (k_block is None) != (v_block is None):
+        raise RuntimeError("rope_kv_write: give k and v destinations together")
+    _require_gpu(cos, sin, *[t for t in (k_cache, v_cache, k_block, v_block, write_start, q_out) if t is not None])
+    if any(t.dtype != dtype for t in (cos, sin, k_cache, v_cache, k_block, v_block, q_out) if t is not None):
+        raise RuntimeError("rope_kv_write: all tensors must share one 16-bit dtype")
+
+    def last_contig(t):
+        return t if t.stride(-1) == 1 and all(st % 8 == 0 for st in t.stride()[:-1]) else t.contiguous()
+    cos, sin = last_contig(cos), last_contig(sin)
+    for name, c in (("k_cache", k_cache), ("v_cache", v_cache), ("k_block", k_block), ("v_block", v_block)):
+        if c is not None and (c.dim() != 4 or c.shape[0] != B or c.shape[2] != Hkv or c.shape[3] != D or
+                              c.stride(-1) != 1):
+            raise RuntimeError(f"rope_kv_write: {name} must be [B, L, Hkv, D] with a contiguous last dim")
+    if k_cache is not None and k_cache.stride() != v_cache.stride():
+        raise RuntimeError("rope_kv_write: k_cache and v_cache strides differ")
+    if k_block is not None and k_block.stride() != v_block.stride():
+        raise RuntimeError("rope_kv_write: k_block and v_block strides differ")
+    if write_start is not None and (write_start.dtype != torch.int32 or not write_start.is_contiguous()):
+        write_start = write_start.to(torch.int32).contiguous()
+    if q_out is None:
+        q_out = torch.empty((B, S, Hq, D), dtype=dtype, device=dev)
+    kv_o = (torch.empty((B, S, Hkv, D), dtype=dtype, device=dev),
+            torch.empty((B, S, Hkv, D), dtype=dtype, device=dev)) if kv_out else (None, None)
+    if sin.stride()[:2] != cos.stride()[:2]:
+        cos, sin = cos.contiguous(), sin.contiguous()
+    d.cos, d.sin = cos.data_ptr(), sin.data_ptr()
+    d.cs_stride_b = cos.stride(0) if cos.shape[0] == B and B > 1 else 0
+    d.cs_stride_s = cos.stride(1)
+    d.q_out, (d.qo_stride_b, d.qo_stride_s, d.qo_stride_h) = q_out.data_ptr(), q_out.stride()[:3]
+    if kv_out:
+        d.k_out, d.v_out = kv_o[0].data_ptr(), kv_o[1].data_ptr()
+        d.ko_stride_b, d.ko_stride_s, d.ko_stride_h = kv_o[0].stride()[:3]
+    if k_cache is not None:
+        d.k_cache, d.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
+        d.c_stride_b, d.c_stride_s, d.c_stride_h = k_cache.stride()[:3]
+        d.cache_len = k_cache.shape[1]
+        d.write_start = _ptr(write_start)
+        d.write_offset = int(write_offset)
+    if k_block is not None:
+        d.k_block, d.v_block = k_block.data_ptr(), v_block.data_ptr()
+        d.bc_stride_b, d.bc_stride_s, d.bc_stride_h = k_block.stride()[:3]
+        d.block_len = k_block.shape[1]
+        d.block_offset = int(block_offset)
+    d.batch, d.seq_len, d.num_q_heads, d.num_kv_heads, d.head_dim = B, S, Hq, Hkv, D
+    d.dtype = _ffi.dtype_code(dtype)
+    return q_out, kv_o, (cos, sin, write_start)
+
+
 def rope_kv_write(
     q: torch.Tensor,
     k: torch.Tensor,
@@ -391,67 +451,76 @@ def rope_kv_write(
     if k.shape[0] != B or k.shape[1] != S or k.shape[3] != D:
         raise RuntimeError("rope_kv_write: q and k/v disagree in batch, length or head_dim")
     Hkv = k.shape[2]
-    if cos.dim() == 2:
-        cos, sin = cos[None], sin[None]
-    if cos.shape != sin.shape or cos.dim() != 3 or cos.shape[1] != S or cos.shape[2] != D or \
-            cos.shape[0] not in (1, B):
-        raise RuntimeError("rope_kv_write: cos / sin must be [1 or B, S, D]")
-    if (k_cache is None) != (v_cache is None) or (k_block is None) != (v_block is None):
-        raise RuntimeError("rope_kv_write: give k and v destinations together")
-    tensors = [q, k, v, cos, sin] + [t for t in (k_cache, v_cache, k_block, v_block, write_start, q_out)
-                                     if t is not None]
-    dev = _require_gpu(*tensors)
-    if q.dtype not in (torch.bfloat16, torch.float16) or any(
-            t.dtype != q.dtype for t in (k, v, cos, sin, k_cache, v_cache, k_block, v_block, q_out) if t is not None):
+    dev = _require_gpu(q, k, v)
+    if q.dtype not in (torch.bfloat16, torch.float16) or k.dtype != q.dtype or v.dtype != q.dtype:
         raise RuntimeError("rope_kv_write: all tensors must share one 16-bit dtype")
+
     def last_contig(t):
         return t if t.stride(-1) == 1 and all(st % 8 == 0 for st in t.stride()[:-1]) else t.contiguous()
-    q, k, v, cos, sin = (last_contig(t) for t in (q, k, v, cos, sin))
-    for name, c in (("k_cache", k_cache), ("v_cache", v_cache), ("k_block", k_block), ("v_block", v_block)):
-        if c is not None and (c.dim() != 4 or c.shape[0] != B or c.shape[2] != Hkv or c.shape[3] != D or
-                              c.stride(-1) != 1):
-            raise RuntimeError(f"rope_kv_write: {name} must be [B, L, Hkv, D] with a contiguous last dim")
-    if k_cache is not None and k_cache.stride() != v_cache.stride():
-        raise RuntimeError("rope_kv_write: k_cache and v_cache strides differ")
-    if k_block is not None and k_block.stride() != v_block.stride():
-        raise RuntimeError("rope_kv_write: k_block and v_block strides differ")
-    if write_start is not None and (write_start.dtype != torch.int32 or not write_start.is_contiguous()):
-        write_start = write_start.to(torch.int32).contiguous()
-    if q_out is None:
-        q_out = torch.empty((B, S, Hq, D), dtype=q.dtype, device=dev)
-    kv_o = (torch.empty((B, S, Hkv, D), dtype=q.dtype, device=dev),
-            torch.empty((B, S, Hkv, D), dtype=q.dtype, device=dev)) if kv_out else (None, None)
+    q, k, v = (last_contig(t) for t in (q, k, v))
     d = _ffi.RopeKVDesc()
+    q_out, kv_o, keep = _rope_dest_desc(d, B, S, Hq, Hkv, D, q.dtype, dev, cos, sin, k_cache, v_cache,
+                                        write_start, write_offset, k_block, v_block, block_offset, q_out, kv_out)
     d.q, (d.q_stride_b, d.q_stride_s, d.q_stride_h) = q.data_ptr(), q.stride()[:3]
     d.k, (d.k_stride_b, d.k_stride_s, d.k_stride_h) = k.data_ptr(), k.stride()[:3]
     d.v, (d.v_stride_b, d.v_stride_s, d.v_stride_h) = v.data_ptr(), v.stride()[:3]
-    d.cos, d.sin = cos.data_ptr(), sin.data_ptr()
-    d.cs_stride_b = cos.stride(0) if cos.shape[0] == B and B > 1 else 0
-    d.cs_stride_s = cos.stride(1)
-    if sin.stride()[:2] != cos.stride()[:2]:
-        sin = sin.contiguous()
-        cos = cos.contiguous()
-        d.cos, d.sin, d.cs_stride_s = cos.data_ptr(), sin.data_ptr(), cos.stride(1)
-        d.cs_stride_b = cos.stride(0) if cos.shape[0] == B and B > 1 else 0
-    d.q_out, (d.qo_stride_b, d.qo_stride_s, d.qo_stride_h) = q_out.data_ptr(), q_out.stride()[:3]
-    if kv_out:
-        d.k_out, d.v_out = kv_o[0].data_ptr(), kv_o[1].data_ptr()
-        d.ko_stride_b, d.ko_stride_s, d.ko_stride_h = kv_o[0].stride()[:3]
-    if k_cache is not None:
-        d.k_cache, d.v_cache = k_cache.data_ptr(), v_cache.data_ptr()
-        d.c_stride_b, d.c_stride_s, d.c_stride_h = k_cache.stride()[:3]
-        d.cache_len = k_cache.shape[1]
-        d.write_start = _ptr(write_start)
-        d.write_offset = int(write_offset)
-    if k_block is not None:
-        d.k_block, d.v_block = k_block.data_ptr(), v_block.data_ptr()
-        d.bc_stride_b, d.bc_stride_s, d.bc_stride_h = k_block.stride()[:3]
-        d.block_len = k_block.shape[1]
-        d.block_offset = int(block_offset)
-    d.batch, d.seq_len, d.num_q_heads, d.num_kv_heads, d.head_dim = B, S, Hq, Hkv, D
-    d.dtype = _ffi.dtype_code(q.dtype)
     rc = _ffi.lib().fdllm_rope_kv_write(ctypes.byref(d), _ffi.stream_ptr(dev))
+    del keep  # launched: the stream orders any reuse of that memory after the kernel
     _ffi.check(rc, "fdllm_rope_kv_write")
+    return (q_out, kv_o) if kv_out else q_out
+
+
+def qkv_rope_kv_write(
+    x: torch.Tensor,
+    wq: torch.Tensor, bq: Optional[torch.Tensor],
+    wk: torch.Tensor, bk: Optional[torch.Tensor],
+    wv: torch.Tensor, bv: Optional[torch.Tensor],
+    cos: torch.Tensor,
+    sin: torch.Tensor,
+    k_cache: Optional[torch.Tensor] = None,
+    v_cache: Optional[torch.Tensor] = None,
+    write_start: Optional[torch.Tensor] = None,
+    write_offset: int = 0,
+    k_block: Optional[torch.Tensor] = None,
+    v_block: Optional[torch.Tensor] = None,
+    block_offset: int = 0,
+    q_out: Optional[torch.Tensor] = None,
+    kv_out: bool = False,
+    head_dim: int = 128,
+):
+    """The q / k / v projections of ``x`` [B, S, hidden] (nn.Linear weights [heads * D,
+    hidden] and biases), then what ``rope_kv_write`` does with them, in one kernel
+    (utils/attention_backends.py:837-842). The projections sum in fp32 and round once
+    after the bias, as a 16-bit linear layer does, in a different order than a library
+    GEMM. head_dim 128, hidden a multiple of 64."""
+    if x.dim() != 3:
+        raise RuntimeError("qkv_rope_kv_write: x must be [B, S, hidden]")
+    B, S, H = x.shape
+    D = head_dim
+    if wq.dim() != 2 or wk.dim() != 2 or wk.shape != wv.shape or wq.shape[1] != H or wk.shape[1] != H or \
+            wq.shape[0] % D or wk.shape[0] % D:
+        raise RuntimeError("qkv_rope_kv_write: weights must be [heads * head_dim, hidden]")
+    Hq, Hkv = wq.shape[0] // D, wk.shape[0] // D
+    for name, b_, w_ in (("bq", bq, wq), ("bk", bk, wk), ("bv", bv, wv)):
+        if b_ is not None and (b_.dim() != 1 or b_.shape[0] != w_.shape[0]):
+            raise RuntimeError(f"qkv_rope_kv_write: {name} must be [{w_.shape[0]}]")
+    ts = [x, wq, wk, wv] + [b_ for b_ in (bq, bk, bv) if b_ is not None]
+    dev = _require_gpu(*ts)
+    if x.dtype not in (torch.bfloat16, torch.float16) or any(t.dtype != x.dtype for t in ts):
+        raise RuntimeError("qkv_rope_kv_write: all tensors must share one 16-bit dtype")
+    if x.stride(-1) != 1 or x.stride(1) % 8 or (B > 1 and x.stride(0) != S * x.stride(1)):
+        x = x.contiguous()
+    wq, wk, wv = (w_.contiguous() for w_ in (wq, wk, wv))
+    bq, bk, bv = (b_.contiguous() if b_ is not None else None for b_ in (bq, bk, bv))
+    d = _ffi.QkvRopeDesc()
+    q_out, kv_o, keep = _rope_dest_desc(d.rope, B, S, Hq, Hkv, D, x.dtype, dev, cos, sin, k_cache, v_cache,
+                                        write_start, write_offset, k_block, v_block, block_offset, q_out, kv_out)
+    d.x, d.x_stride_row, d.hidden = x.data_ptr(), x.stride(1), H
+    d.wq, d.wk, d.wv = wq.data_ptr(), wk.data_ptr(), wv.data_ptr()
+    d.bq, d.bk, d.bv = _ptr(bq), _ptr(bk), _ptr(bv)
+    rc = _ffi.lib().fdllm_qkv_rope_kv_write(ctypes.byref(d), _ffi.stream_ptr(dev))
+    del keep  # launched: the stream orders any reuse of that memory after the kernel
+    _ffi.check(rc, "fdllm_qkv_rope_kv_write")
     return (q_out, kv_o) if kv_out else q_out
 
 

@@ -169,12 +169,24 @@ def _apply_rotary_pos_emb(q, k, cos, sin):
 # The patched forward uses ops.rope_kv_write where it applies (False: RoPE in torch
 # and separate cache writes, the statement of the reference's code).
 FUSED_ROPE_CACHE_WRITE = True
+# True: with the fused RoPE + cache write, the q / k / v projections run in the same
+# kernel (ops.qkv_rope_kv_write) where head_dim is 128, hidden a multiple of 64 and the
+# call has at most FUSED_QKV_MAX_TOKENS token rows. Off by default: the projections are
+# then three nn.Linear calls, as in the reference's code, and bit-identical to them; the
+# fused kernel sums in another order, so its projections differ from a library GEMM's
+# in the last bit of about 1 % of the values. On the 7B layout it takes 40.5 us against
+# 53 us for three hipBLASLt GEMMs + the RoPE kernel at 512 and at 128 rows, but 113
+# against 99 us at 2048 rows, where the library GEMMs' larger tiles win.
+FUSED_QKV_PROJECTION = False
+FUSED_QKV_MAX_TOKENS = 1024
 
 
-def _fused_rope_cache_write(q, k, v, cos, sin, layer_idx, cache, update, block_cache, replace_position):
-    """RoPE + the cache writes of the patched forward in one kernel (ops.rope_kv_write);
-    returns the rotated q, or None (nothing done) where the call is not one of the
-    three forms below, which then take the unfused path.
+def _fused_rope_cache_write(rope, S, cos, layer_idx, cache, update, block_cache, replace_position):
+    """RoPE + the cache writes of the patched forward in one kernel; ``rope(k_cache,
+    v_cache, **destinations)`` launches it (ops.rope_kv_write on projected q / k / v, or
+    ops.qkv_rope_kv_write with the projections included) and returns the rotated q.
+    Returns None (nothing launched) where the call is not one of the three forms below,
+    which then take the unfused path.
 
     * commit (update_past_key_values, no block cache): rows at the committed length;
     * diffusion step, no block cache: rows at kv_write_start (write_scratch_compiled);
@@ -184,22 +196,19 @@ def _fused_rope_cache_write(q, k, v, cos, sin, layer_idx, cache, update, block_c
       the other rows there, so writing the new rows alone leaves the same cache. The
       first forward of a block (the block cache's update) must cover the whole block.
     Writes through ops.kv_cache_write and the attention are unchanged."""
-    if not isinstance(cache, StaticKVCache) or q.dtype not in (torch.bfloat16, torch.float16) or \
-            q.shape[-1] % 16 != 0 or cos.dim() != 3:
+    if not isinstance(cache, StaticKVCache) or cos.dim() != 3:
         return None
-    S = k.shape[1]
+    kc, vc = cache.key_cache[layer_idx], cache.value_cache[layer_idx]
     if update:
         if block_cache is not None:
             return None
         start = cache.get_seq_length()
-        q_rot = ops.rope_kv_write(q, k, v, cos, sin, cache.key_cache[layer_idx], cache.value_cache[layer_idx],
-                                  write_offset=start)
+        q_rot = rope(kc, vc, write_offset=start)
         cache.note_update(S, layer_idx)
         cache.set_scratch_seqlens(start + S)
         return q_rot
     if block_cache is None:
-        return ops.rope_kv_write(q, k, v, cos, sin, cache.key_cache[layer_idx], cache.value_cache[layer_idx],
-                                 write_start=cache._write_start)
+        return rope(kc, vc, write_start=cache._write_start)
     kb, vb = block_cache[layer_idx]
     if len(block_cache) <= layer_idx:
         if S != kb.shape[1]:
@@ -207,12 +216,22 @@ def _fused_rope_cache_write(q, k, v, cos, sin, layer_idx, cache, update, block_c
         rp = 0
     else:
         rp = 0 if replace_position is None else int(replace_position)
-    q_rot = ops.rope_kv_write(q, k, v, cos, sin, cache.key_cache[layer_idx], cache.value_cache[layer_idx],
-                              write_start=cache._write_start, write_offset=rp, k_block=kb, v_block=vb,
-                              block_offset=rp)
+    q_rot = rope(kc, vc, write_start=cache._write_start, write_offset=rp, k_block=kb, v_block=vb, block_offset=rp)
     if len(block_cache) <= layer_idx:
         block_cache.note_update(layer_idx)
     return q_rot
+
+
+def _fusable(attn_module, hidden_states, head_dim):
+    """The 16-bit shapes the fused kernels take: RoPE + cache write need head_dim a
+    multiple of 16; the fused projections need head_dim 128, hidden a multiple of 64 and
+    16-bit nn.Linear weights."""
+    dt = hidden_states.dtype
+    rope_ok = dt in (torch.bfloat16, torch.float16) and head_dim % 16 == 0
+    proj_ok = (rope_ok and FUSED_QKV_PROJECTION and head_dim == 128 and hidden_states.shape[-1] % 64 == 0 and
+               hidden_states[..., 0].numel() <= FUSED_QKV_MAX_TOKENS and
+               all(getattr(attn_module, n).weight.dtype == dt for n in ("q_proj", "k_proj", "v_proj")))
+    return rope_ok, proj_ok
 
 
 def _create_patched_attention_forward(attn_module, attn_backend, static_block_cache=None):
@@ -235,17 +254,35 @@ def _create_patched_attention_forward(attn_module, attn_backend, static_block_ca
                                     replace_position, **kwargs)
         input_shape = hidden_states.shape[:-1]
         hidden_shape = (*input_shape, -1, head_dim)
-        q = attn_module.q_proj(hidden_states).view(hidden_shape)
-        k = attn_module.k_proj(hidden_states).view(hidden_shape)
-        v = attn_module.v_proj(hidden_states).view(hidden_shape)
         cos, sin = position_embeddings
+        fused = attn_backend.name == AttentionBackend.HIP and FUSED_ROPE_CACHE_WRITE
+        rope_ok, proj_ok = _fusable(attn_module, hidden_states, head_dim) if fused else (False, False)
+        if proj_ok and hidden_states.dim() == 3:
+            qp, kp, vp = attn_module.q_proj, attn_module.k_proj, attn_module.v_proj
 
-        if attn_backend.name == AttentionBackend.HIP and FUSED_ROPE_CACHE_WRITE:
-            q = _fused_rope_cache_write(q, k, v, cos, sin, layer_idx, past_key_value, update_past_key_values,
-                                        block_past_key_values, replace_position)
+            def rope(kc, vc, **dst):
+                return ops.qkv_rope_kv_write(hidden_states, qp.weight, qp.bias, kp.weight, kp.bias, vp.weight,
+                                             vp.bias, cos, sin, kc, vc, head_dim=head_dim, **dst)
+            q = _fused_rope_cache_write(rope, hidden_states.shape[1], cos, layer_idx, past_key_value,
+                                        update_past_key_values, block_past_key_values, replace_position)
             if q is not None:
                 full_k, full_v = past_key_value.get_full_kv(layer_idx)
                 out = attn_backend.flash_kvcache_attention(q, full_k, full_v,
+                                                           cache_seqlens=past_key_value.scratch_seqlens,
+                                                           is_causal=False, scaling=scaling)
+                return attn_module.o_proj(out.reshape(*input_shape, -1))
+        q = attn_module.q_proj(hidden_states).view(hidden_shape)
+        k = attn_module.k_proj(hidden_states).view(hidden_shape)
+        v = attn_module.v_proj(hidden_states).view(hidden_shape)
+
+        if rope_ok:
+            def rope(kc, vc, **dst):
+                return ops.rope_kv_write(q, k, v, cos, sin, kc, vc, **dst)
+            q_rot = _fused_rope_cache_write(rope, k.shape[1], cos, layer_idx, past_key_value,
+                                            update_past_key_values, block_past_key_values, replace_position)
+            if q_rot is not None:
+                full_k, full_v = past_key_value.get_full_kv(layer_idx)
+                out = attn_backend.flash_kvcache_attention(q_rot, full_k, full_v,
                                                            cache_seqlens=past_key_value.scratch_seqlens,
                                                            is_causal=False, scaling=scaling)
                 return attn_module.o_proj(out.reshape(*input_shape, -1))

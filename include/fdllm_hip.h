@@ -341,6 +341,46 @@ typedef struct fdllm_rope_kv_desc {
 int fdllm_rope_kv_write(const fdllm_rope_kv_desc* desc, void* stream);
 
 /* -------------------------------------------------------------------------
+ * The q / k / v projections of the new tokens fused with the RoPE + KV cache
+ * write above: the projection GEMMs with RoPE and the cache write as their
+ * epilogue.
+ *
+ *   for token row r = b * seq_len + t (r < batch * seq_len):
+ *     q[b, t, h] = round(x[r] . wq[h * D + i] + bq[h * D + i])   i < D (= 128)
+ *     k[b, t, g], v[b, t, g] likewise with wk / bk, wv / bv
+ *   then everything fdllm_rope_kv_write does with q, k, v (outputs, caches,
+ *   positions and rounding as there).
+ *
+ * x is [batch * seq_len, hidden] with row stride x_stride_row (elements, a
+ * multiple of 8, at least hidden); wq is [num_q_heads * D, hidden] and wk / wv
+ * [num_kv_heads * D, hidden], rows contiguous (nn.Linear weights); biases are
+ * [heads * D] or NULL. Products are summed in fp32 (MFMA), the bias added in
+ * fp32 and the sum rounded once to `dtype`, as a 16-bit linear layer with bias
+ * does; the summation order differs from a library GEMM's, so q / k / v agree
+ * with separate projections to within the rounding of their last bit. In
+ * `rope`, q / k / v and their strides are not read; head_dim must be 128 and
+ * hidden a multiple of 64.
+ *
+ * Replaces: the q_proj / k_proj / v_proj calls of the patched attention forward
+ * (utils/attention_backends.py:837-839, :946-948; the layers of modeling.py:321-323)
+ * together with the RoPE and cache writes that fdllm_rope_kv_write replaces.
+ * ------------------------------------------------------------------------- */
+typedef struct fdllm_qkv_rope_desc {
+  const void* x;
+  int64_t x_stride_row;
+  const void* wq;
+  const void* wk;
+  const void* wv;
+  const void* bq; /* or NULL */
+  const void* bk;
+  const void* bv;
+  int hidden;
+  fdllm_rope_kv_desc rope;
+} fdllm_qkv_rope_desc;
+
+int fdllm_qkv_rope_kv_write(const fdllm_qkv_rope_desc* desc, void* stream);
+
+/* -------------------------------------------------------------------------
  * One greedy sampling + threshold unmasking step of a sub-block.
  *
  *   for b < batch, i < num_positions (<= 64):

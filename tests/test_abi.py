@@ -73,12 +73,13 @@ def test_descriptor_layout_matches_c_struct():
     assert ctypes.sizeof(d) % 8 == 0
 
 
-@pytest.mark.parametrize("struct", ["fdllm_kv_attn_desc", "fdllm_rope_kv_desc"])
+@pytest.mark.parametrize("struct", ["fdllm_kv_attn_desc", "fdllm_rope_kv_desc", "fdllm_qkv_rope_desc"])
 def test_descriptor_offsets_match_the_c_compiler(tmp_path, struct):
     """Every field offset and the size of the ctypes mirrors equal what gcc lays out
     for the structs of include/fdllm_hip.h."""
     from fast_v2_amd import _ffi
-    mirror = {"fdllm_kv_attn_desc": _ffi.KVAttnDesc, "fdllm_rope_kv_desc": _ffi.RopeKVDesc}[struct]
+    mirror = {"fdllm_kv_attn_desc": _ffi.KVAttnDesc, "fdllm_rope_kv_desc": _ffi.RopeKVDesc,
+              "fdllm_qkv_rope_desc": _ffi.QkvRopeDesc}[struct]
     fields = [f[0] for f in mirror._fields_]
     prog = tmp_path / "layout.c"
     lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{ROOT / "include" / "fdllm_hip.h"}"',
@@ -129,6 +130,18 @@ def test_rejected_arguments_launch_nothing(lib):
     assert lib.fdllm_rope_kv_write(ctypes.byref(r), None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
     r.head_dim = 128  # no tensors given
     assert lib.fdllm_rope_kv_write(ctypes.byref(r), None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    assert b"null" in lib.fdllm_last_error()
+    # fused projections: head_dim other than 128, hidden not a multiple of 64, no tensors
+    qd = _ffi.QkvRopeDesc()
+    qd.rope.batch, qd.rope.seq_len, qd.rope.num_q_heads, qd.rope.num_kv_heads = 1, 1, 28, 4
+    qd.rope.dtype, qd.rope.head_dim, qd.hidden, qd.x_stride_row = _ffi.DTYPE_BF16, 64, 3584, 3584
+    assert lib.fdllm_qkv_rope_kv_write(ctypes.byref(qd), None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    assert b"head_dim" in lib.fdllm_last_error()
+    qd.rope.head_dim, qd.hidden, qd.x_stride_row = 128, 3584 + 32, 3584 + 32
+    assert lib.fdllm_qkv_rope_kv_write(ctypes.byref(qd), None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
+    assert b"multiple of 64" in lib.fdllm_last_error()
+    qd.hidden, qd.x_stride_row = 3584, 3584
+    assert lib.fdllm_qkv_rope_kv_write(ctypes.byref(qd), None) == _ffi.FDLLM_ERR_INVALID_ARGUMENT
     assert b"null" in lib.fdllm_last_error()
     # residual add + norm: hidden size not a multiple of 8; SiLU product: ragged length
     rc = lib.fdllm_add_rmsnorm(None, None, None, 0, None, None, 4, 100, 1e-6, _ffi.DTYPE_BF16, _ffi.NORM_PLAIN, None)

@@ -89,12 +89,155 @@ def test_fused_forward_equals_unfused(gpu, use_block_cache):
     model = em.build_model(cfg, gpu)
     x = torch.randint(0, cfg.vocab_size - 1, (4, 64), generator=torch.Generator().manual_seed(4)).to(gpu)
     outs = []
-    for fused in (True, False):
-        ab.FUSED_ROPE_CACHE_WRITE = fused
-        try:
-            out, st = es.generate(model, x, max_new_tokens=96, use_block_cache=use_block_cache,
-                                  impl=es.HipStaticAttention(graphs=False))
-        finally:
-            ab.FUSED_ROPE_CACHE_WRITE = True
-        outs.append(out)
+    saved = ab.FUSED_QKV_PROJECTION
+    ab.FUSED_QKV_PROJECTION = False  # projections by nn.Linear on both sides: RoPE + writes compared alone
+    try:
+        for fused in (True, False):
+            ab.FUSED_ROPE_CACHE_WRITE = fused
+            try:
+                out, st = es.generate(model, x, max_new_tokens=96, use_block_cache=use_block_cache,
+                                      impl=es.HipStaticAttention(graphs=False))
+            finally:
+                ab.FUSED_ROPE_CACHE_WRITE = True
+            outs.append(out)
+    finally:
+        ab.FUSED_QKV_PROJECTION = saved
     assert torch.equal(outs[0], outs[1])
+
+
+# ---------------------------------------------------------------------------
+# q / k / v projections fused with RoPE + cache write (fdllm_qkv_rope_kv_write)
+
+def _qkv_case(B, S, H, Hq, Hkv, dtype, gpu, exact, seed, x_pad=0):
+    """x [B, S, H] (a view with row stride H + x_pad), weights [heads * 128, H], biases.
+    exact: small multiples of 1/16 whose products and sums are exact in fp32, so every
+    summation order gives the same projection and the result is fixed bit for bit."""
+    g = torch.Generator().manual_seed(seed)
+    D = 128
+    if exact:
+        def mk(*shape):
+            return (torch.randint(-4, 5, shape, generator=g).float() / 16).to(dtype)
+        xf = torch.randint(-3, 4, (B, S, H + x_pad), generator=g).float().to(dtype)
+        wq, wk, wv = mk(Hq * D, H), mk(Hkv * D, H), mk(Hkv * D, H)
+        bq, bk, bv = mk(Hq * D), mk(Hkv * D), mk(Hkv * D)
+    else:
+        xf = torch.randn(B, S, H + x_pad, generator=g).to(dtype)
+        wq, wk, wv = ((torch.randn(n * D, H, generator=g) * 0.02).to(dtype) for n in (Hq, Hkv, Hkv))
+        bq, bk, bv = ((torch.randn(n * D, generator=g) * 0.1).to(dtype) for n in (Hq, Hkv, Hkv))
+    t = [u.to(gpu) for u in (xf, wq, bq, wk, bk, wv, bv)]
+    x = t[0][..., :H]
+    return x, t[1:]
+
+
+def _ulps(a, b):
+    ai = a.contiguous().view(torch.int16).to(torch.int32)
+    bi = b.contiguous().view(torch.int16).to(torch.int32)
+    ai = torch.where(ai < 0, -(ai & 0x7FFF), ai)
+    bi = torch.where(bi < 0, -(bi & 0x7FFF), bi)
+    return (ai - bi).abs()
+
+
+@pytest.mark.parametrize("B,S,H,Hq,Hkv,dtype,x_pad", [
+    (16, 32, 3584, 28, 4, torch.bfloat16, 0),   # the 7B full-block forward: 512 token rows
+    (16, 8, 3584, 28, 4, torch.bfloat16, 0),    # the 7B sub-block forward: 128 rows
+    (3, 37, 256, 4, 2, torch.bfloat16, 64),     # 111 rows: one ragged tile; padded x rows
+    (5, 64, 512, 2, 1, torch.float16, 0),       # 320 rows: three tiles, the last ragged
+])
+def test_qkv_rope_exact_inputs_bit_exact(gpu, B, S, H, Hq, Hkv, dtype, x_pad):
+    """With inputs whose products and sums are exact in fp32, the fused kernel equals
+    the projections (float64, rounded once to the 16-bit type, as a linear layer with
+    bias rounds) + the eager RoPE + the cache writes bit for bit: a transposed operand,
+    a wrong row, column or head, a dropped bias or K step would all show."""
+    D = 128
+    x, (wq, bq, wk, bk, wv, bv) = _qkv_case(B, S, H, Hq, Hkv, dtype, gpu, True, B * S + H, x_pad)
+    cos, sin = _tables(S, D, 517, dtype, gpu)
+    L, LB = S + 40, max(S, 32)
+    ws = torch.arange(B, dtype=torch.int32, device=gpu) * 3
+    kc = torch.full((B, L, Hkv, D), 7.0, dtype=dtype, device=gpu)
+    vc = kc.clone()
+    kb = torch.full((B, LB, Hkv, D), -5.0, dtype=dtype, device=gpu)
+    vb = kb.clone()
+    print(f"case qkv exact B={B} S={S} H={H} {Hq}/{Hkv} {dtype}", flush=True)
+    q_rot, (k_rot, v_out) = ops.qkv_rope_kv_write(x, wq, bq, wk, bk, wv, bv, cos, sin, kc, vc, write_start=ws,
+                                                  write_offset=1, k_block=kb, v_block=vb, block_offset=0,
+                                                  kv_out=True)
+    x64 = x.double().cpu()  # exact: float64 holds every sum, so this is the projection
+
+    def proj(w, b_, n):
+        return (x64 @ w.double().cpu().T + b_.double().cpu()).to(dtype).view(B, S, n, D).to(gpu)
+    q, k, v = proj(wq, bq, Hq), proj(wk, bk, Hkv), proj(wv, bv, Hkv)
+    q_ref, k_ref = _rope_torch(q, cos, sin), _rope_torch(k, cos, sin)
+    assert torch.equal(v_out, v)
+    assert torch.equal(q_rot, q_ref)
+    assert torch.equal(k_rot, k_ref)
+    kc_ref, vc_ref = torch.full_like(kc, 7.0), torch.full_like(vc, 7.0)
+    for b in range(B):
+        p0 = int(ws[b]) + 1
+        n = max(0, min(S, L - p0))  # rows past the cache's length are skipped
+        kc_ref[b, p0:p0 + n], vc_ref[b, p0:p0 + n] = k_ref[b, :n], v[b, :n]
+    assert torch.equal(kc, kc_ref) and torch.equal(vc, vc_ref)
+    kb_ref, vb_ref = torch.full_like(kb, -5.0), torch.full_like(vb, -5.0)
+    kb_ref[:, :S], vb_ref[:, :S] = k_ref, v
+    assert torch.equal(kb, kb_ref) and torch.equal(vb, vb_ref)
+
+
+@pytest.mark.parametrize("S", [32, 8])
+def test_qkv_rope_random_weights_within_rounding(gpu, S):
+    """7B shapes with N(0, 0.02) weights: the projections agree with a float64
+    restatement rounded to bf16 to within one ulp or the fp32 sum's rounding error near
+    zero (fp32 MFMA sums in another order can round the other way), 99 % of them
+    exactly, and the rotated rows with the eager RoPE of those projections to within
+    what one flipped input can move them."""
+    B, H, Hq, Hkv, D = 16, 3584, 28, 4, 128
+    x, (wq, bq, wk, bk, wv, bv) = _qkv_case(B, S, H, Hq, Hkv, torch.bfloat16, gpu, False, S)
+    cos, sin = _tables(S, D, 700, torch.bfloat16, gpu)
+    print(f"case qkv random S={S}", flush=True)
+    q_rot, (k_rot, v_out) = ops.qkv_rope_kv_write(x, wq, bq, wk, bk, wv, bv, cos, sin, kv_out=True)
+    x64 = x.double().cpu()
+
+    def proj(w, b_, n):
+        return (x64 @ w.double().cpu().T + b_.double().cpu()).to(torch.bfloat16).view(B, S, n, D)
+    v_ref = proj(wv, bv, Hkv)
+    got = v_out.cpu()
+    du = _ulps(got, v_ref)
+    # one ulp of the result, or the fp32 sum's own error near zero (|y| ~ 1e-3 has ulps
+    # of 1e-5, below the rounding error of 3584 fp32 additions of terms ~0.02)
+    ulp = v_ref.float().abs() * 2.0 ** -7
+    assert bool(((got.float() - v_ref.float()).abs() <= ulp + 1e-4).all())
+    assert float((du == 0).float().mean()) > 0.99
+    q_ref = _rope_torch(proj(wq, bq, Hq).to(gpu), cos, sin).cpu()
+    k_ref = _rope_torch(proj(wk, bk, Hkv).to(gpu), cos, sin).cpu()
+    for got, ref in ((q_rot.cpu(), q_ref), (k_rot.cpu(), k_ref)):
+        torch.testing.assert_close(got.float(), ref.float(), atol=2e-2, rtol=2e-2)
+        assert float((_ulps(got, ref) == 0).float().mean()) > 0.98
+
+
+def test_qkv_fused_forward_matches_unfused(gpu):
+    """The patched forward with the fused projections against nn.Linear projections +
+    the fused RoPE: the logits of a prefill and of a diffusion step agree to within the
+    projections' last-bit rounding."""
+    cfg = em.BlockDiffusionConfig(num_hidden_layers=2)
+    model = em.build_model(cfg, gpu)
+    x = torch.randint(0, cfg.vocab_size - 1, (4, 96), generator=torch.Generator().manual_seed(6)).to(gpu)
+    logits = []
+    saved = ab.FUSED_QKV_PROJECTION
+    for fused in (True, False):
+        ab.FUSED_QKV_PROJECTION = fused
+        try:
+            cache, _ = es.HipStaticAttention(graphs=False).make_caches(4, 256, cfg, torch.bfloat16, gpu, False)
+            orig = ab.patch_attention_layers(model, ab.get_attention_backend("hip"))
+            try:
+                pre = model(x[:, :64], cache, update_past_key_values=True).float()
+                cache.set_kv_write_start(64)
+                cache.set_scratch_seqlens(96)
+                step = model(x[:, 64:96], cache, cache_position=torch.arange(64, 96, device=gpu)).float()
+            finally:
+                ab.unpatch_attention_layers(model, orig)
+        finally:
+            ab.FUSED_QKV_PROJECTION = saved
+        logits.append((pre, step))
+    for a, b in zip(logits[0], logits[1]):
+        rel = float((a - b).norm() / b.norm())
+        assert rel < 2e-2, rel
+        assert float((a.argmax(-1) == b.argmax(-1)).float().mean()) > 0.9
+
