@@ -291,3 +291,39 @@ def test_cache_write_matches_slice_assignment_and_paging():
     for b in range(B):
         back = np.concatenate([pool2[pt[b, i]] for i in range(per)], axis=0)
         assert np.array_equal(back, exp[b].numpy())
+
+
+def test_e2e_oracle_caches_follow_the_static_cache_rules():
+    """The eager e2e oracle's caches: update() stores at the committed length and moves
+    it only after the last layer (static_kv_cache.py:132-160); write_scratch_compiled()
+    stores at kv_write_start without moving it (:218-229); the block cache's write()
+    stores at the block offset. Each equals cache_write_np's per-sequence store; a
+    planted pointer move after the first layer would fail the second layer's rows."""
+    from oracle.e2e_eager import TorchBlockCache, TorchKVCache
+    g = torch.Generator().manual_seed(11)
+    B, L, H, D, layers = 2, 24, 2, 8, 3
+    c = TorchKVCache(B, L, layers, H, D, torch.float32, "cpu")
+    k1, v1 = torch.randn(B, 5, H, D, generator=g), torch.randn(B, 5, H, D, generator=g)
+    for layer in range(layers):
+        before = c.key_cache[layer].clone()
+        c.update(k1 + layer, v1 - layer, layer)
+        exp = oa.cache_write_np(before.numpy(), (k1 + layer).numpy(), [0, 0])
+        np.testing.assert_array_equal(c.key_cache[layer].numpy(), exp)
+        assert c.get_seq_length() == (5 if layer == layers - 1 else 0)
+    k2 = torch.randn(B, 3, H, D, generator=g)
+    for layer in range(layers):
+        before = c.key_cache[layer].clone()
+        c.update(k2, k2, layer)
+        np.testing.assert_array_equal(c.key_cache[layer].numpy(), oa.cache_write_np(before.numpy(), k2.numpy(), [5, 5]))
+    assert c.get_seq_length() == 8
+    c.set_kv_write_start(8)
+    k3 = torch.randn(B, 4, H, D, generator=g)
+    before = c.value_cache[1].clone()
+    c.write_scratch_compiled(k3, k3, 1)
+    np.testing.assert_array_equal(c.value_cache[1].numpy(), oa.cache_write_np(before.numpy(), k3.numpy(), [8, 8]))
+    assert c.get_seq_length() == 8
+    bc = TorchBlockCache(B, 32, layers, H, D, torch.float32, "cpu")
+    kb = torch.randn(B, 8, H, D, generator=g)
+    before = bc.key_cache[2].clone()
+    bc.write(kb, kb, 2, 16)
+    np.testing.assert_array_equal(bc.key_cache[2].numpy(), oa.cache_write_np(before.numpy(), kb.numpy(), [16, 16]))
