@@ -368,6 +368,50 @@ def bench_prefill(torch, args):
     return res
 
 
+def bench_qkv(torch, args):
+    """The q / k / v projections of one 7B-layout layer with RoPE and the static-cache
+    write: the fused kernel (ops.qkv_rope_kv_write) against three nn.Linear GEMMs +
+    ops.rope_kv_write, for the full-block (16 x 32), sub-block (16 x 8) and a 4 x 512
+    prefill forward; 28 layers' weights cycled so each call reads its weights from HBM,
+    both forms timed in rotation. Not part of the default run (``--only qkv``)."""
+    from fast_v2_amd import ops
+
+    dev = torch.device("cuda", 0)
+    H, Hq, Hkv, D, layers = 3584, 28, 4, 128, 28
+    g = torch.Generator(device=dev).manual_seed(0)
+    W = [[(torch.randn(n * D, H, device=dev, generator=g) * 0.02).to(torch.bfloat16) for n in (Hq, Hkv, Hkv)]
+         for _ in range(layers)]
+    Bs = [[(torch.randn(n * D, device=dev, generator=g) * 0.1).to(torch.bfloat16) for n in (Hq, Hkv, Hkv)]
+          for _ in range(layers)]
+    res = {}
+    for B, S in ((16, 32), (16, 8), (4, 512)):
+        x = torch.randn(B, S, H, device=dev, generator=g).to(torch.bfloat16)
+        inv = 1.0 / (1e6 ** (torch.arange(0, D, 2, device=dev).float() / D))
+        emb = torch.cat([torch.arange(S, device=dev).float()[:, None] * inv[None]] * 2, -1)
+        cos, sin = emb.cos().to(torch.bfloat16)[None], emb.sin().to(torch.bfloat16)[None]
+        kc = torch.zeros(B, S + 64, Hkv, D, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        ws = torch.zeros(B, dtype=torch.int32, device=dev)
+
+        def fused(i):
+            w, b = W[i % layers], Bs[i % layers]
+            ops.qkv_rope_kv_write(x, w[0], b[0], w[1], b[1], w[2], b[2], cos, sin, kc, vc, write_start=ws)
+
+        def unfused(i):
+            w, b = W[i % layers], Bs[i % layers]
+            q = torch.nn.functional.linear(x, w[0], b[0]).view(B, S, Hq, D)
+            k = torch.nn.functional.linear(x, w[1], b[1]).view(B, S, Hkv, D)
+            v = torch.nn.functional.linear(x, w[2], b[2]).view(B, S, Hkv, D)
+            ops.rope_kv_write(q, k, v, cos, sin, kc, vc, write_start=ws)
+        us = _time_graphs_rotating(torch, {"fused": fused, "unfused": unfused}, 2 * layers, 2, rounds=3)
+        flops = 2.0 * B * S * H * (Hq + 2 * Hkv) * D
+        res[f"{B}x{S}"] = {"us_fused": us["fused"], "us_linear_then_rope": us["unfused"],
+                           "tflops_fused": flops / (us["fused"] * 1e-6) / 1e12}
+    del W, Bs
+    torch.cuda.empty_cache()
+    return res
+
+
 def bench_e2e(torch, args):
     """End-to-end block-diffusion generation with the random-init 7B-layout model on the
     HIP path: batch 16, 512-token prompts, ``--e2e-tokens`` new tokens, 32-token blocks,
@@ -597,7 +641,7 @@ def main() -> int:
                          "or the same cache stored head-major")
     ap.add_argument("--no-check", action="store_true", help="skip the graph-vs-eager equality check")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["decode", "decode_full", "gather", "prefill", "e2e"], default=None)
+    ap.add_argument("--only", choices=["decode", "decode_full", "gather", "prefill", "e2e", "qkv"], default=None)
     ap.add_argument("--e2e-tokens", type=int, default=1024, help="tokens generated in the end-to-end leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end generation leg")
     ap.add_argument("--e2e-weights", default=None,
@@ -655,6 +699,10 @@ def main() -> int:
         _log(f"prefill: {extra['prefill']['us_per_call']:.1f} us per call with the cache write, "
              f"{extra['prefill']['roofline']['achieved']:.0f} TFLOP/s")
 
+    if args.only == "qkv":
+        extra["qkv_projection"] = bench_qkv(torch, args)
+        _log("qkv: " + ", ".join(f"{k} fused {v['us_fused']:.1f} us / linear + rope {v['us_linear_then_rope']:.1f} us"
+                                  for k, v in extra["qkv_projection"].items()))
     if args.only == "e2e" or (args.only is None and not args.no_e2e):
         extra["e2e"] = bench_e2e(torch, args)
         _log(f"e2e: {extra['e2e']['tokens_per_s']} tokens/s ({extra['e2e']['forwards']} forwards, "
