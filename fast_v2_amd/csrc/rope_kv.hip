@@ -132,10 +132,11 @@ __global__ __launch_bounds__(256) void rope_kv_kernel(const RopeArgs a) {
 // q / k / v projections with RoPE and the cache writes as their epilogue
 // (fdllm_qkv_rope_kv_write).
 //
-// Workgroup = one 128-token x 128-column tile of one head's projection (so the RoPE
-// partners i and i + 64 are in the tile), 4 waves as 2 x 2 of 64 x 64; the head's
-// 128 weight rows and the 128 token rows stream through a ring of four LDS slots of
-// 64-deep K steps (direct-to-LDS loads, three steps in flight, one barrier per step);
+// Workgroup = one tile of 128 tokens x one head's 128 columns (or, with few tiles, half
+// of them: 32 columns and their RoPE partners 64 further on), so the RoPE partners i and
+// i + 64 are in the tile; 4 waves as 2 x 2; the weight rows and the 128 token rows stream
+// through a ring of LDS slots of 64-deep K steps (direct-to-LDS loads, all but two slots'
+// steps in flight, one barrier per step);
 // v_mfma_f32_32x32x16 with both operands read from LDS (XOR-swizzled 16-byte chunks,
 // chunk p of row r at p ^ ((r >> 1) & 7), so the 16 lanes of a read phase hit 16
 // distinct bank groups). A wave's two column tiles are columns j and j + 64 of the
@@ -149,7 +150,7 @@ struct QkvArgs {
   fdllm_qkv_rope_desc d;
   int T;        // token rows: batch * seq_len
   int n_mt;     // 128-row token tiles
-  int n_tiles;  // n_mt * (num_q_heads + 2 num_kv_heads)
+  int n_tiles;  // n_mt * (num_q_heads + 2 num_kv_heads) * workgroups per (head, token tile)
   int per_xcd;  // ceil(n_tiles / 8)
 };
 
@@ -159,22 +160,27 @@ struct QkvArgs {
 #ifndef FDLLM_QKV_KT
 #define FDLLM_QKV_KT 64
 #endif
+
 constexpr int kQkvBM = 128;  // token rows per tile (and head_dim: columns per tile)
 constexpr int kQkvKT = FDLLM_QKV_KT;  // K step per LDS slot (64 or 32)
 constexpr int kQkvYS = 136;  // epilogue tile row stride (elements; 272 bytes)
 
-template <typename T, bool F16>
+// BN: columns of one head per workgroup (128: the whole head; 64: two workgroups per
+// head, each with 32 columns and their RoPE partners 64 further on); NS: LDS ring slots.
+template <typename T, bool F16, int BN, int NS>
 __global__ __launch_bounds__(256) void qkv_rope_kernel(const QkvArgs a) {
   constexpr int KT = kQkvKT;
+  constexpr int kQkvParts = 128 / BN;      // workgroups per (head, token tile)
+  constexpr int NT = BN / 64;              // 32-column MFMA tiles per wave
   constexpr int ROWB = KT * 2;             // bytes of one row of an operand tile
   constexpr int CH = ROWB / 16;            // 16-byte chunks per row
   constexpr int RPD = 1024 / ROWB;         // rows one direct-to-LDS load (1 KB per wave) covers
-  constexpr int NDMA = kQkvBM / RPD / 4;   // loads per wave per operand tile
-  constexpr int TB = kQkvBM * ROWB;        // bytes of one operand tile
-  constexpr int SLOT = 2 * TB;             // token rows, then weight rows
-  constexpr int NS = 131072 / SLOT;        // slots in the 128 KB ring
+  constexpr int NDX = kQkvBM / RPD / 4;    // loads per wave of the token tile
+  constexpr int NDW = BN / RPD / 4;        // loads per wave of the weight tile
+  constexpr int TB = kQkvBM * ROWB;        // bytes of the token tile
+  constexpr int SLOT = TB + BN * ROWB;     // token rows, then weight rows
   constexpr int KK = KT / 16;              // MFMA k-steps per slot
-  static_assert(NS >= 3 && CH >= 4, "ring shape");
+  static_assert(NS >= 3 && CH >= 4 && NDW >= 1 && NS * SLOT <= 131072, "ring shape");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[NS * SLOT];
   static_assert(kQkvBM * kQkvYS * 2 <= NS * SLOT, "epilogue tile fits the ring");
   const fdllm_qkv_rope_desc& d = a.d;
@@ -182,8 +188,13 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(const QkvArgs a) {
 
   const int tile = static_cast<int>(blockIdx.x & 7) * a.per_xcd + static_cast<int>(blockIdx.x >> 3);
   if (tile >= a.n_tiles) return;  // uniform over the workgroup
-  const int head = tile / a.n_mt;  // q heads, then k heads, then v heads
-  const int mt = tile - head * a.n_mt;
+  const int head = tile / (a.n_mt * kQkvParts);  // q heads, then k heads, then v heads
+  const int part = (tile - head * a.n_mt * kQkvParts) / a.n_mt;
+  const int mt = tile - (head * kQkvParts + part) * a.n_mt;
+  const int c0 = part * (BN / 2);  // first column of each half this workgroup computes
+  // head column of weight-tile row rw: the first BN / 2 rows are columns c0.., the rest
+  // their RoPE partners 64 further on (the identity for a whole head)
+  auto hcol = [c0](int rw) __attribute__((always_inline)) { return rw < BN / 2 ? c0 + rw : 64 + c0 + rw - BN / 2; };
   const int Hq = r.num_q_heads, Hkv = r.num_kv_heads;
   const int kind = head < Hq ? 0 : (head < Hq + Hkv ? 1 : 2);
   const int hh = kind == 0 ? head : (kind == 1 ? head - Hq : head - Hq - Hkv);
@@ -209,72 +220,77 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(const QkvArgs a) {
   auto swz = [](int row) __attribute__((always_inline)) { return (row / (256 / ROWB)) & (CH - 1); };
   // load i of wave w fills rows RPD (NDMA w + i) .. + RPD of both tiles: lane -> row
   // + lane / CH, LDS chunk lane % CH
-  int xoff[NDMA], woff[NDMA];
+  int xoff[NDX], woff[NDW];
 #pragma unroll
-  for (int i = 0; i < NDMA; ++i) {
-    const int row = RPD * (NDMA * wave + i) + lane / CH;
-    const int chunk = (lane % CH) ^ swz(row);
-    xoff[i] = row * xs_row * 2 + chunk * 16;
-    woff[i] = row * K * 2 + chunk * 16;
+  for (int i = 0; i < NDX; ++i) {
+    const int row = RPD * (NDX * wave + i) + lane / CH;
+    xoff[i] = row * xs_row * 2 + (((lane % CH) ^ swz(row)) * 16);
+  }
+#pragma unroll
+  for (int i = 0; i < NDW; ++i) {
+    const int row = RPD * (NDW * wave + i) + lane / CH;
+    woff[i] = hcol(row) * K * 2 + (((lane % CH) ^ swz(row)) * 16);
   }
   const uint32_t lds0 = static_cast<uint32_t>(reinterpret_cast<uintptr_t>(lds));
   auto issue = [&](int st, int slot) __attribute__((always_inline)) {
     const bool live = st < nk;  // uniform
     const int kb = st * ROWB;
-    const uint32_t dst = lds0 + slot * SLOT + NDMA * wave * 1024;
+    const uint32_t dst = lds0 + slot * SLOT;
 #pragma unroll
-    for (int i = 0; i < NDMA; ++i) lds_dma16(live ? xsrd : zsrd, xoff[i] + kb, dst + i * 1024);
+    for (int i = 0; i < NDX; ++i) lds_dma16(live ? xsrd : zsrd, xoff[i] + kb, dst + (NDX * wave + i) * 1024);
 #pragma unroll
-    for (int i = 0; i < NDMA; ++i) lds_dma16(live ? wsrd : zsrd, woff[i] + kb, dst + TB + i * 1024);
+    for (int i = 0; i < NDW; ++i) lds_dma16(live ? wsrd : zsrd, woff[i] + kb, dst + TB + (NDW * wave + i) * 1024);
   };
 
-  // operand reads: wave (wm, wn) takes token rows 64 wm + 32 m2 + lane % 32 and head
-  // columns 64 n2 + 32 wn + lane % 32; lane / 32 picks the upper 8 of each 16-deep step
+  // operand reads: wave (wm, wn) takes token rows 64 wm + 32 m2 + lane % 32 and weight-
+  // tile rows 64 n2 + 32 wn + lane % 32; lane / 32 picks the upper 8 of each 16-deep step
   const int wm = wave & 1, wn = wave >> 1;
   const int l32 = lane & 31, kh = lane >> 5;
-  int arow[2], brow[2];
+  int arow[2], brow[NT];
 #pragma unroll
-  for (int i = 0; i < 2; ++i) {
-    arow[i] = 64 * wm + 32 * i + l32;
-    brow[i] = 64 * i + 32 * wn + l32;
-  }
-  f32x16 acc[2][2];
+  for (int i = 0; i < 2; ++i) arow[i] = 64 * wm + 32 * i + l32;
+#pragma unroll
+  for (int j = 0; j < NT; ++j) brow[j] = 64 * j + 32 * wn + l32;
+  f32x16 acc[2][NT];
 #pragma unroll
   for (int i = 0; i < 2; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < NT; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
 
   auto compute = [&](int slot) __attribute__((always_inline)) {
     const uint8_t* sx = lds + slot * SLOT;
     const uint8_t* sw = sx + TB;
-    u32x4 av[KK][2], bv[KK][2];
+    u32x4 av[KK][2], bv[KK][NT];
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk) {
       const int chunk = 2 * kk + kh;
 #pragma unroll
-      for (int i = 0; i < 2; ++i) {
+      for (int i = 0; i < 2; ++i)
         av[kk][i] = *reinterpret_cast<const u32x4*>(sx + arow[i] * ROWB + ((chunk ^ swz(arow[i])) << 4));
-        bv[kk][i] = *reinterpret_cast<const u32x4*>(sw + brow[i] * ROWB + ((chunk ^ swz(brow[i])) << 4));
-      }
+#pragma unroll
+      for (int j = 0; j < NT; ++j)
+        bv[kk][j] = *reinterpret_cast<const u32x4*>(sw + brow[j] * ROWB + ((chunk ^ swz(brow[j])) << 4));
     }
 #pragma unroll
     for (int kk = 0; kk < KK; ++kk)
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16<F16>(av[kk][i], bv[kk][j], acc[i][j]);
+        for (int j = 0; j < NT; ++j) acc[i][j] = mfma32x32x16<F16>(av[kk][i], bv[kk][j], acc[i][j]);
 #if FDLLM_QKV_SCHED
-    // the step's operand reads go out QA ahead of the MFMAs that use them
-    constexpr int QA = FDLLM_QKV_SCHED < 4 * KK ? FDLLM_QKV_SCHED : 4 * KK;
-    __builtin_amdgcn_sched_group_barrier(0x100, QA, 0);  // DS reads
+    if constexpr (NT == 2) {
+      // the step's operand reads go out QA ahead of the MFMAs that use them
+      constexpr int QA = FDLLM_QKV_SCHED < 4 * KK ? FDLLM_QKV_SCHED : 4 * KK;
+      __builtin_amdgcn_sched_group_barrier(0x100, QA, 0);  // DS reads
 #pragma unroll
-    for (int i = 0; i < 4 * KK - QA; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      for (int i = 0; i < 4 * KK - QA; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, QA, 0);
     }
-    __builtin_amdgcn_sched_group_barrier(0x008, QA, 0);
 #endif
   };
 
@@ -284,7 +300,7 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(const QkvArgs a) {
 #pragma unroll
   for (int st = 0; st < NS - 1; ++st) issue(st, st);
   for (int j = 0; j < nk; ++j) {
-    wait_vmcnt<(NS - 2) * 2 * NDMA>();  // this thread's loads of step j have landed
+    wait_vmcnt<(NS - 2) * (NDX + NDW)>();  // this thread's loads of step j have landed
     lds_barrier();                        // ... and every thread's; every wave is done with step j - 1
     issue(j + NS - 1, (j + NS - 1) % NS);
     compute(j % NS);
@@ -295,8 +311,8 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(const QkvArgs a) {
   // ---- epilogue: y = to_dtype(acc + bias) into the tile Y[row][col]
   uint16_t* Y = reinterpret_cast<uint16_t*>(lds);
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int col = brow[j];
+  for (int j = 0; j < NT; ++j) {
+    const int col = hcol(brow[j]);
     const float bcol = bias != nullptr ? Elt<T>::lo(static_cast<uint32_t>(bias[hh * kQkvBM + col])) : 0.f;
 #pragma unroll
     for (int i = 0; i < 2; ++i)
@@ -308,12 +324,13 @@ __global__ __launch_bounds__(256) void qkv_rope_kernel(const QkvArgs a) {
   }
   lds_barrier();
 
-  // ---- rotation and stores: item = (token row, 8-dimension block c < 64)
+  // ---- rotation and stores: item = (token row, 8-dimension block c in the first half)
   const int S = r.seq_len;
   constexpr int half = kQkvBM / 2;
-  for (int it = tid; it < kQkvBM * 8; it += 256) {
-    const int rr = it >> 3;
-    const int c = (it & 7) * 8;
+  constexpr int NB = BN / 16;  // 8-dimension blocks per row in each half of this workgroup
+  for (int it = tid; it < kQkvBM * NB; it += 256) {
+    const int rr = it / NB;
+    const int c = c0 + (it % NB) * 8;
     if (rr >= rows) break;  // items are row-major: every later item is past the end too
     const int tok = row0 + rr;
     const int b = tok / S;
@@ -419,12 +436,22 @@ extern "C" int fdllm_qkv_rope_kv_write(const fdllm_qkv_rope_desc* d, void* strea
   a.T = static_cast<int>(T);
   a.n_mt = static_cast<int>((T + kQkvBM - 1) / kQkvBM);
   const int heads = r.num_q_heads + 2 * r.num_kv_heads;
-  FDLLM_CHECK_ARG(static_cast<int64_t>(a.n_mt) * heads < (int64_t{1} << 30), "fdllm_qkv_rope_kv_write: too many tiles");
-  a.n_tiles = a.n_mt * heads;
+  FDLLM_CHECK_ARG(static_cast<int64_t>(a.n_mt) * heads * 2 < (int64_t{1} << 30), "fdllm_qkv_rope_kv_write: too many tiles");
+  // Whole-head tiles while they give the compute units more than half a workgroup each;
+  // with fewer (the 128-row sub-block forward: 36 tiles), half-head tiles, twice as many
+  // workgroups each streaming 3/4 of the bytes: 29 against 41 us on the 7B layout (at 512
+  // rows the half-head form, 288 workgroups for 256 compute units, took 55 against 40 us).
+  const bool half_head = a.n_mt * heads <= 128;
+  a.n_tiles = a.n_mt * heads * (half_head ? 2 : 1);
   a.per_xcd = (a.n_tiles + 7) / 8;
   const dim3 grid(static_cast<unsigned>(8 * a.per_xcd));
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (r.dtype == FDLLM_DTYPE_BF16) qkv_rope_kernel<bf16_t, false><<<grid, dim3(256), 0, s>>>(a);
-  else qkv_rope_kernel<f16_t, true><<<grid, dim3(256), 0, s>>>(a);
+  if (r.dtype == FDLLM_DTYPE_BF16) {
+    if (half_head) qkv_rope_kernel<bf16_t, false, 64, 5><<<grid, dim3(256), 0, s>>>(a);
+    else qkv_rope_kernel<bf16_t, false, 128, 4><<<grid, dim3(256), 0, s>>>(a);
+  } else {
+    if (half_head) qkv_rope_kernel<f16_t, true, 64, 5><<<grid, dim3(256), 0, s>>>(a);
+    else qkv_rope_kernel<f16_t, true, 128, 4><<<grid, dim3(256), 0, s>>>(a);
+  }
   FDLLM_RETURN_LAUNCH_STATUS("fdllm_qkv_rope_kv_write");
 }

@@ -174,9 +174,9 @@ FUSED_ROPE_CACHE_WRITE = True
 # call has at most FUSED_QKV_MAX_TOKENS token rows. Off by default: the projections are
 # then three nn.Linear calls, as in the reference's code, and bit-identical to them; the
 # fused kernel sums in another order, so its projections differ from a library GEMM's
-# in the last bit of about 1 % of the values. On the 7B layout it takes 40.5 us against
-# 53 us for three hipBLASLt GEMMs + the RoPE kernel at 512 and at 128 rows, but 113
-# against 99 us at 2048 rows, where the library GEMMs' larger tiles win.
+# in the last bit of about 1 % of the values. On the 7B layout it takes 40 us against
+# 53 us for three hipBLASLt GEMMs + the RoPE kernel at 512 rows and 29 against 53 us at
+# 128 rows, but 117 against 99 us at 2048 rows, where the library GEMMs' larger tiles win.
 FUSED_QKV_PROJECTION = False
 FUSED_QKV_MAX_TOKENS = 1024
 
