@@ -255,3 +255,18 @@ def test_timeline_phase_statistics():
     assert math.isclose(res["span"], 19.5)
     assert np.allclose(res["d_loop"], (7.8, 11.0, 11.5))
     assert np.allclose(res["d_merge"], (2.5, 2.5, 2.5))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N with N > 1 prints one JSON line saying the build targets one GPU
+    and exits with status 2, before touching torch or a device."""
+    import json
+    import subprocess
+    import sys
+    from pathlib import Path
+    root = Path(__file__).resolve().parents[1]
+    out = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                         timeout=120, cwd=root)
+    assert out.returncode == 2
+    line = json.loads(out.stdout.strip().splitlines()[-1])
+    assert line["n_gpus"] == 2 and "one GPU" in line["error"]
