@@ -368,6 +368,25 @@ def bench_prefill(torch, args):
     return res
 
 
+def bench_small_fp32(torch, args):
+    """Config 1 on the GPU: the fp32 attention kernel on the fp32 workload (batch 1, 32
+    queries x 12 / 2 heads over 512 + 32 keys, head_dim 128), the call as the caller
+    makes it (one graph node per call)."""
+    from fast_v2_amd import ops, workloads
+
+    dev = torch.device("cuda", 0)
+    wl = workloads.kv_decode_fp32_small(seed=0)
+    q, k, v, sl = wl.q.to(dev), wl.k_cache.to(dev), wl.v_cache.to(dev), wl.seqlens.to(dev)
+    out = torch.empty_like(q)
+
+    def step(i):
+        ops.block_attn(q, k, v, sl, wl.scale, out=out)
+    us = _time_graph(torch, step, 200, 4)
+    flops = 4 * 32 * 12 * 128 * 544
+    return {"us_per_call": us, "gflops": flops / (us * 1e-6) / 1e9,
+            "workload": "fp32, q [1, 32, 12, 128] over 544 keys of 2 KV heads (kv_attn_f32_kernel)"}
+
+
 def bench_qkv(torch, args):
     """The q / k / v projections of one 7B-layout layer with RoPE and the static-cache
     write: the fused kernel (ops.qkv_rope_kv_write) against three nn.Linear GEMMs +
@@ -694,6 +713,9 @@ def main() -> int:
         _log(f"gather: normed {g['normed']['us_per_call']:.3f} us, pair {g['pair']['us_per_call']:.3f} us; "
              f"plain copy of the rows {g['ceiling']['copy_us_per_call']:.3f} us, empty kernel node "
              f"{g['ceiling']['empty_kernel_us_per_node']:.3f} us")
+    if args.only is None:
+        extra["small_fp32"] = bench_small_fp32(torch, args)
+        _log(f"small fp32 (config 1): {extra['small_fp32']['us_per_call']:.2f} us per call")
     if args.only in (None, "prefill"):
         extra["prefill"] = bench_prefill(torch, args)
         _log(f"prefill: {extra['prefill']['us_per_call']:.1f} us per call with the cache write, "

@@ -1372,34 +1372,62 @@ __device__ __forceinline__ float halves_sum(float v) {
 // fp32 attention: fp32 inputs, fp32 output, fp32 arithmetic throughout (the reference's
 // CPU path runs the SDPA shim in fp32, e.g. a 12 / 2-head, 128-dim block of 32 queries over
 // 544 keys; tests/test_focus.py:205-228). Every mask mode, contiguous or paged, any GQA.
-// One wave per (sequence, query token, query head): for the scores lane = key of a 64-key
-// chunk (each lane a full dot product from its key row, the query row broadcast from
-// LDS); for the output lane = head dimension (DPL of them), the chunk's probabilities
-// taken lane by lane with readlane. Online softmax in base 2 (scores pre-multiplied by
-// scale * log2 e), rescaled whenever the chunk maximum moves it.
+// Workgroup = 4 query rows of one (sequence, KV head) (rows r = t G + g of its Sq x G
+// rows), one per wave. Each 64-key chunk of K and V is loaded once per workgroup,
+// coalesced, into LDS (K rows padded to D + 4 floats, so the 16 lanes of a read phase hit
+// distinct banks), the next chunk's loads in flight in registers meanwhile. Scores: lane
+// = key, a full dot product (four partial sums) from its K row in LDS against the wave's
+// query row (broadcast from LDS); output: lane = head dimension (DPL of them), the chunk's
+// probabilities written to LDS and read back as broadcasts, V rows read from LDS. Online softmax in
+// base 2 (scores pre-multiplied by scale * log2 e), rescaled whenever the chunk maximum
+// moves it. The workgroup runs to the largest key bound of its rows; each row masks the
+// keys past its own.
+// query rows per wave of kv_attn_f32_kernel: on the 12 / 2-head block of 32 queries over
+// 544 keys, 1: 27.8 us, 2: 36.2 us, 4: 72.9 us (fewer rows per workgroup, more workgroups
+// in flight; the previous one-wave-per-row form without staging: 85 us)
+#ifndef FDLLM_F32_ROWS_PER_WAVE
+#define FDLLM_F32_ROWS_PER_WAVE 1
+#endif
 template <int DPL, bool PAGED>
 __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
   constexpr int D = 64 * DPL;
-  __shared__ __attribute__((aligned(16))) float sq[4][D];
-  const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
-  const int b = blockIdx.y;
-  const int rows = p.Sq * p.Hq;
-  const int row = static_cast<int>(blockIdx.x) * 4 + w;  // t * Hq + hq
-  const bool live = row < rows;                           // wave-uniform
-  const int rr = live ? row : rows - 1;
-  const int t = rr / p.Hq;
-  const int hq = rr - t * p.Hq;
-  const int kvh = hq / p.G;
+  constexpr int KS = D + 4;   // K row stride in LDS (floats)
+  constexpr int RW = FDLLM_F32_ROWS_PER_WAVE;  // rows per wave
+  constexpr int RWG = 4 * RW; // rows per workgroup
+  constexpr int CK = 64;      // keys per chunk
+  constexpr int PER = CK * D / 4 / 256;  // 16-byte loads per thread per chunk and tensor
+  __shared__ __attribute__((aligned(16))) float sK[CK * KS];
+  __shared__ __attribute__((aligned(16))) float sV[CK * D];
+  __shared__ __attribute__((aligned(16))) float sQ[RWG][D];
+  __shared__ float sP[RWG][CK];  // the chunk's probabilities of each row
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
+  const int b = blockIdx.z;
+  const int kvh = blockIdx.y;
+  const int R = p.Sq * p.G;
+  const int r0 = static_cast<int>(blockIdx.x) * RWG;
   int seqlen = p.seqlens[b];
   if (seqlen > p.max_seqlen) seqlen = p.max_seqlen;
   if (PAGED && seqlen > p.max_pages * p.page_size) seqlen = p.max_pages * p.page_size;
   if (seqlen < 0) seqlen = 0;
   const int qs = p.q_start ? p.q_start[b] : seqlen - p.Sq;
-  const int lim = __builtin_amdgcn_readfirstlane(row_key_limit(p, seqlen, qs, t));
-  const float* q = reinterpret_cast<const float*>(p.q) + b * p.q_sb + t * p.q_ss + hq * p.q_sh;
-  for (int i = lane; i < D; i += 64) sq[w][i] = q[i];
-  __syncthreads();
+  // key bounds never decrease with the query token, so the workgroup's last row has the largest
+  const int kv_end = __builtin_amdgcn_readfirstlane(row_key_limit(p, seqlen, qs, (min(r0 + RWG, R) - 1) / p.G));
+
+  int lim[RW], tq[RW], hq[RW];
+  bool live[RW];
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    const int r = r0 + w * RW + i;
+    live[i] = r < R;  // wave-uniform
+    const int rc = live[i] ? r : R - 1;
+    tq[i] = rc / p.G;
+    hq[i] = kvh * p.G + (rc - tq[i] * p.G);
+    lim[i] = __builtin_amdgcn_readfirstlane(row_key_limit(p, seqlen, qs, tq[i]));
+    const float* q = reinterpret_cast<const float*>(p.q) + b * p.q_sb + tq[i] * p.q_ss + hq[i] * p.q_sh;
+    for (int d = lane; d < D; d += 64) sQ[w * RW + i][d] = q[d];
+  }
   const float* kb = reinterpret_cast<const float*>(p.k) + kvh * p.k_sh;
   const float* vb = reinterpret_cast<const float*>(p.v) + kvh * p.v_sh;
   auto row_off = [&](int key, bool kcache) -> int64_t {
@@ -1411,47 +1439,96 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
       return static_cast<int64_t>(b) * (kcache ? p.k_sp : p.v_sp) + static_cast<int64_t>(key) * ss;
     }
   };
-  float o[DPL];
+  // load e of a thread: f32x4 index tid + 256 e of the chunk = key idx / (D / 4), column
+  // 4 (idx % (D / 4)); keys at or past kv_end read as zero
+  f32x4 kr[PER], vr[PER];
+  auto load_chunk = [&](int k0) {
 #pragma unroll
-  for (int j = 0; j < DPL; ++j) o[j] = 0.f;
-  float m = -INFINITY, l = 0.f;
-  for (int k0 = 0; k0 < lim; k0 += 64) {
-    const int key = k0 + lane;
-    float s = -INFINITY;
-    if (key < lim) {
-      const float* kr = kb + row_off(key, true);
-      float acc = 0.f;
-#pragma unroll 8
-      for (int i = 0; i < D; i += 4) {
-        const f32x4 kv = *reinterpret_cast<const f32x4*>(kr + i);
-        const f32x4 qv = *reinterpret_cast<const f32x4*>(&sq[w][i]);
-        acc = fmaf(qv[0], kv[0], acc);
-        acc = fmaf(qv[1], kv[1], acc);
-        acc = fmaf(qv[2], kv[2], acc);
-        acc = fmaf(qv[3], kv[3], acc);
+    for (int e = 0; e < PER; ++e) {
+      const int idx = tid + 256 * e;
+      const int key = k0 + idx / (D / 4);
+      const int c = 4 * (idx % (D / 4));
+      if (key < kv_end) {
+        kr[e] = *reinterpret_cast<const f32x4*>(kb + row_off(key, true) + c);
+        vr[e] = *reinterpret_cast<const f32x4*>(vb + row_off(key, false) + c);
+      } else {
+        kr[e] = f32x4{0.f, 0.f, 0.f, 0.f};
+        vr[e] = f32x4{0.f, 0.f, 0.f, 0.f};
       }
-      s = acc * p.scale_log2;
     }
-    const float m_new = fmaxf(m, wave_allreduce_max(s));
-    const float alpha = m == -INFINITY ? 0.f : fast_exp2(m - m_new);
-    const float pk = key < lim ? fast_exp2(s - m_new) : 0.f;
-    l = l * alpha + wave_allreduce_sum(pk);
+  };
+  float o[RW][DPL], m[RW], l[RW];
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) o[j] *= alpha;
-    const int nk = min(64, lim - k0);
-    for (int kk = 0; kk < nk; ++kk) {
-      const float pkk = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(pk), kk));
-      const float* vr = vb + row_off(k0 + kk, false);
+  for (int i = 0; i < RW; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) o[j] = fmaf(pkk, vr[lane + 64 * j], o[j]);
-    }
-    m = m_new;
+    for (int j = 0; j < DPL; ++j) o[i][j] = 0.f;
   }
-  if (live) {
-    float* out = reinterpret_cast<float*>(p.out) + b * p.o_sb + t * p.o_ss + hq * p.o_sh;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
+  if (kv_end > 0) load_chunk(0);
+  for (int k0 = 0; k0 < kv_end; k0 += CK) {
+    __syncthreads();  // every wave is done with the previous chunk (and sQ is written)
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) out[lane + 64 * j] = o[j] * inv;
+    for (int e = 0; e < PER; ++e) {
+      const int idx = tid + 256 * e;
+      const int key = idx / (D / 4);
+      const int c = 4 * (idx % (D / 4));
+      *reinterpret_cast<f32x4*>(&sK[key * KS + c]) = kr[e];
+      *reinterpret_cast<f32x4*>(&sV[key * D + c]) = vr[e];
+    }
+    __syncthreads();
+    if (k0 + CK < kv_end) load_chunk(k0 + CK);  // in flight during this chunk's math
+    const int key = k0 + lane;
+    // four partial sums per row (independent FMA chains), added at the end
+    float acc[RW][4];
+#pragma unroll
+    for (int i = 0; i < RW; ++i)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[i][u] = 0.f;
+#pragma unroll 8
+    for (int d = 0; d < D; d += 4) {
+      const f32x4 kv = *reinterpret_cast<const f32x4*>(&sK[lane * KS + d]);
+#pragma unroll
+      for (int i = 0; i < RW; ++i) {
+        const f32x4 qv = *reinterpret_cast<const f32x4*>(&sQ[w * RW + i][d]);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[i][u] = fmaf(qv[u], kv[u], acc[i][u]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      const float dot = (acc[i][0] + acc[i][1]) + (acc[i][2] + acc[i][3]);
+      const float sc = key < lim[i] ? dot * p.scale_log2 : -INFINITY;
+      const float m_new = fmaxf(m[i], wave_allreduce_max(sc));
+      const float alpha = m[i] == -INFINITY ? 0.f : fast_exp2(m[i] - m_new);
+      const float pk = key < lim[i] ? fast_exp2(sc - m_new) : 0.f;
+      sP[w * RW + i][lane] = pk;  // read back by this wave only, as broadcasts
+      l[i] = l[i] * alpha + wave_allreduce_sum(pk);
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) o[i][j] *= alpha;
+      m[i] = m_new;
+    }
+    const int nk = min(CK, kv_end - k0);
+    for (int kk = 0; kk < nk; ++kk) {
+      float v[DPL];
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) v[j] = sV[kk * D + lane + 64 * j];
+#pragma unroll
+      for (int i = 0; i < RW; ++i) {
+        const float pkk = sP[w * RW + i][kk];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) o[i][j] = fmaf(pkk, v[j], o[i][j]);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < RW; ++i) {
+    if (live[i]) {
+      float* out = reinterpret_cast<float*>(p.out) + b * p.o_sb + tq[i] * p.o_ss + hq[i] * p.o_sh;
+      const float inv = l[i] > 0.f ? 1.f / l[i] : 0.f;
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) out[lane + 64 * j] = o[i][j] * inv;
+    }
   }
 }
 
@@ -2820,7 +2897,7 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
     pl->kind = kPlanF32;
     pl->decode = false;
     pl->MT = 0;
-    pl->rows_per_wg = 4;
+    pl->rows_per_wg = 4 * FDLLM_F32_ROWS_PER_WAVE;
     pl->n_rb = 1;
     pl->n_splits = 1;
     pl->chunk = 0;
@@ -3239,9 +3316,12 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
   const bool f16 = d->dtype == FDLLM_DTYPE_F16;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (pl.kind == kPlanF32) {
-    const int64_t rows = static_cast<int64_t>(d->q_len) * d->num_q_heads;
+    // 4 FDLLM_F32_ROWS_PER_WAVE rows of one (sequence, KV head) per workgroup
+    constexpr int rwg = 4 * FDLLM_F32_ROWS_PER_WAVE;
+    const int64_t rows = static_cast<int64_t>(d->q_len) * (d->num_q_heads / d->num_kv_heads);
     FDLLM_CHECK_ARG(d->batch < 65536, "fdllm_kv_attn_fwd: batch too large");
-    const dim3 grid(static_cast<unsigned>((rows + 3) / 4), static_cast<unsigned>(d->batch));
+    const dim3 grid(static_cast<unsigned>((rows + rwg - 1) / rwg), static_cast<unsigned>(d->num_kv_heads),
+                    static_cast<unsigned>(d->batch));
     const bool paged = d->page_table != nullptr;
     if (d->head_dim == 128) {
       if (paged) kv_attn_f32_kernel<2, true><<<grid, dim3(256), 0, s>>>(p);
