@@ -114,6 +114,32 @@ def _time_graphs_rotating(torch, step_fns: dict, steps: int, warmup: int, rounds
     return {name: sorted(t)[len(t) // 2] for name, t in times.items()}
 
 
+_PROBES = None
+
+
+def _probes():
+    """ctypes handle of lib/libfdllm_probes.so (the measurement probes: include/fdllm_probes.h)."""
+    global _PROBES
+    if _PROBES is None:
+        import ctypes
+        path = ROOT / "fast_v2_amd" / "lib" / "libfdllm_probes.so"
+        if not path.exists():
+            raise RuntimeError(f"{path} is not built; run `python -m fast_v2_amd.build`")
+        lib = ctypes.CDLL(str(path))
+        vp, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32
+        lib.fdllm_probe_read_kv.argtypes = [vp, vp, i64, i64, i64, i64, i64, i64, vp, i32, i32, vp,
+                                            ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+        lib.fdllm_probe_read_kv.restype = ctypes.c_int
+        lib.fdllm_probe_copy_rows.argtypes = [vp, i64, ctypes.c_int, vp, vp, ctypes.c_int, ctypes.c_int, vp]
+        lib.fdllm_probe_copy_rows.restype = ctypes.c_int
+        _PROBES = lib
+    return _PROBES
+
+
+def _stream_ptr(torch):
+    return torch.cuda.current_stream().cuda_stream
+
+
 def _traffic(name: str):
     try:
         data = json.loads(TRAFFIC_FILE.read_text())
@@ -148,6 +174,12 @@ def bench_decode(torch, args):
     pt = wl.page_table.to(dev)
     sl = wl.seqlens.to(dev)
     page_size = wl.page_size
+    if args.layout == "paged_hm":
+        # head-major pages: each page stored [Hkv, page_size, D], so one KV head's page is one
+        # contiguous run (page_size x D x 2 B); viewed as [num_pages, page_size, Hkv, D]
+        kp = kp.permute(0, 1, 3, 2, 4).contiguous().permute(0, 1, 3, 2, 4)
+        vp = vp.permute(0, 1, 3, 2, 4).contiguous().permute(0, 1, 3, 2, 4)
+        torch.cuda.empty_cache()
     if args.layout in ("contig", "bhsd"):
         # the reference's static cache layout [B, max_S, Hkv, D] per layer (identity pages)
         B = q.shape[0]
@@ -171,14 +203,46 @@ def bench_decode(torch, args):
     def step(i):
         layer = i % layers
         ops.block_attn(q, kp[layer], vp[layer], sl, wl.scale, page_table=pt, page_size=page_size,
-                       out=out, kv_split=args.kv_split)
+                       out=out, kv_split=args.kv_split, balanced_splits=args.balanced_splits)
 
-    # graph replay must reproduce the eager result bit for bit
-    step(layers - 1)
+    # graph replay must reproduce the eager result bit for bit: the last captured step
+    # reads layer (steps - 1) % layers, the eager reference the same layer
+    step(args.steps - 1)
     eager = out.clone()
     us = _time_graph(torch, step, args.steps, args.warmup)
-    if args.steps % layers == 0 and not args.no_check and not torch.equal(out, eager):
+    if not args.no_check and not torch.equal(out, eager):
         raise RuntimeError("graph replay output differs from the eager call")
+    extra_layouts = {}
+    if args.layout == "paged_hm":
+        # the same values in token-major pages ([page_size, Hkv, D] per page, the paged layout
+        # of flash_attn_with_kvcache's block table), timed the same way
+        kt = kp.contiguous()
+        vt = vp.contiguous()
+
+        def step_tm(i):
+            ops.block_attn(q, kt[i % layers], vt[i % layers], sl, wl.scale, page_table=pt, page_size=page_size,
+                           out=out, kv_split=args.kv_split, balanced_splits=args.balanced_splits)
+
+        extra_layouts["us_per_step_token_major_pages"] = _time_graph(torch, step_tm, args.steps, args.warmup)
+        del kt, vt
+        torch.cuda.empty_cache()
+    # the practical floor of the call: a plain read of the same K/V bytes in the same tile
+    # pattern and launch shape (one KV head per workgroup, 32-key tiles, 64 slots per head),
+    # no math, timed through the same graph path
+    probes = _probes()
+    sink = torch.zeros(4, dtype=torch.int32, device=dev)
+    kst, vst = kp[0].stride(), vp[0].stride()
+
+    def read_step(i):
+        layer = i % layers
+        rc = probes.fdllm_probe_read_kv(kp[layer].data_ptr(), vp[layer].data_ptr(), kst[0], kst[1], kst[2],
+                                        vst[0], vst[1], vst[2], pt.data_ptr() if pt is not None else None,
+                                        pt.shape[1] if pt is not None else 0, page_size, sl.data_ptr(), B, Hkv,
+                                        max(8, (256 // Hkv + 7) // 8 * 8), sink.data_ptr(), _stream_ptr(torch))
+        if rc != 0:
+            raise RuntimeError(f"fdllm_probe_read_kv failed ({rc})")
+
+    us_read = _time_graph(torch, read_step, args.steps, args.warmup)
     nbytes = workloads.decode_bytes(wl.seqlens, Hq, Hkv, D, Sq)
     flops = workloads.decode_flops(wl.seqlens, Hq, D, Sq)
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -191,6 +255,16 @@ def bench_decode(torch, args):
         "roofline": _roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s", _traffic("kv_attn_decode_bs16")),
         "us_per_model_step_28_layers": us * LAYERS,
         "seqlens": wl.seqlens.tolist(),
+        "layout": args.layout,
+        **extra_layouts,
+        "ceiling": {
+            "read_us_per_step": us_read,
+            "read_bytes": nbytes - workloads.decode_bytes(wl.seqlens * 0, Hq, Hkv, D, Sq),
+            "step_vs_read": us / us_read,
+            "note": ("plain read of every visible K/V row of the step (fdllm_probe_read_kv: one KV head per "
+                     "workgroup, 32-key tiles, two tiles in flight per team, keys dealt evenly over 64 slots "
+                     "per head, no math), same pages and layer pools, same graph path"),
+        },
     }
     del q, kp, vp, pt, sl, out
     torch.cuda.empty_cache()
@@ -289,15 +363,23 @@ def bench_gather(torch, args):
                                            _traffic(f"gather_rmsnorm_{name}"))}
     # The practical ceiling of a call this size, timed the same way (graph of the same
     # number of nodes, inputs rotated through the same 48 HBM-resident slabs): a plain
-    # device copy of the bytes the gather moves (the 1024 x 3584 rows read and written,
-    # torch's copy kernel), and an empty kernel node (torch.cuda._sleep(0)).
-    T, H = idx.shape[1], wl.hidden.shape[2]
-    src = [h[0, :T] for h in hs]
+    # gathered copy of the same rows (fdllm_probe_copy_rows: dst[t] = hidden[idx[t]], one
+    # wave per row, all loads before the stores; the normed call's bytes less the 15 KB of
+    # weight and indices), and an empty kernel node (torch.cuda._sleep(0)).
+    T, H, S = idx.shape[1], wl.hidden.shape[2], wl.hidden.shape[1]
     dst = torch.empty((T, H), dtype=wl.hidden.dtype, device=dev)
+    probes = _probes()
 
     def copy_step(i):
-        dst.copy_(src[i % copies])
+        rc = probes.fdllm_probe_copy_rows(hs[i % copies].data_ptr(), H * 2, S, idx.data_ptr(), dst.data_ptr(), T,
+                                          H * 2, _stream_ptr(torch))
+        if rc != 0:
+            raise RuntimeError(f"fdllm_probe_copy_rows failed ({rc})")
 
+    copy_step(0)
+    torch.cuda.synchronize()
+    if not torch.equal(dst, wl.hidden[0, wl.indices[0]].to(dev)):
+        raise RuntimeError("the probe copy does not reproduce the gathered rows")
     us_copy = _time_graph(torch, copy_step, args.gather_steps, min(args.warmup, 32))
     us_empty = _time_graph(torch, lambda i: torch.cuda._sleep(0), args.gather_steps, min(args.warmup, 32))
     copy_bytes = 2 * T * H * 2
@@ -306,11 +388,12 @@ def bench_gather(torch, args):
         "copy_gbs": copy_bytes / (us_copy * 1e-6) / 1e9,
         "empty_kernel_us_per_node": us_empty,
         "normed_vs_copy": res["normed"]["us_per_call"] / us_copy,
-        "note": ("plain copy of the 1024 x 3584 bf16 rows (read + write, the normed call's bytes less "
-                 "the 15 KB of weight and indices) and an empty kernel node, each as a graph of the same "
-                 "length as the gather's"),
+        "note": ("gathered copy of the 1024 x 3584 bf16 rows by a hand-written gfx950 kernel "
+                 "(fdllm_probe_copy_rows: one wave per row, every load issued before the stores; read + "
+                 "write, the normed call's bytes less the 15 KB of weight and indices) and an empty kernel "
+                 "node, each as a graph of the same length as the gather's"),
     }
-    del hs, src, dst
+    del hs, dst
     torch.cuda.empty_cache()
     return res
 
@@ -655,10 +738,12 @@ def main() -> int:
     ap.add_argument("--prefill-steps", type=int, default=20)
     ap.add_argument("--kv-split", type=int, default=0, help="keys per split-KV work item (0 = automatic)")
     ap.add_argument("--layers", type=int, default=LAYERS, help="layer pools cycled by the decode steps")
-    ap.add_argument("--layout", choices=["paged", "contig", "bhsd"], default="paged",
-                    help="KV layout: 32-token pages, the contiguous [B, max_S, Hkv, D] static cache, "
-                         "or the same cache stored head-major")
+    ap.add_argument("--layout", choices=["paged", "paged_hm", "contig", "bhsd"], default="paged_hm",
+                    help="KV layout: 32-token pages (token-major), 32-token pages stored head-major, the "
+                         "contiguous [B, max_S, Hkv, D] static cache, or the same cache stored head-major")
     ap.add_argument("--no-check", action="store_true", help="skip the graph-vs-eager equality check")
+    ap.add_argument("--balanced-splits", action="store_true",
+                    help="decode: deal all sequences' keys evenly over the workgroups (runs across sequences)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", choices=["decode", "decode_full", "gather", "prefill", "e2e", "qkv"], default=None)
     ap.add_argument("--e2e-tokens", type=int, default=1024, help="tokens generated in the end-to-end leg")
@@ -764,16 +849,20 @@ def main() -> int:
             "data": "synthetic",
             "config": {
                 "workload": ("block-decode attention, 7B geometry: batch 16, 28 query / 4 KV heads, head_dim 128, "
-                             "prefix U{1024..4096 step 32} + 32-token block, 8 active queries, 32-token pages, "
-                             "one layer per step over 28 layer pools"),
+                             "prefix U{1024..4096 step 32} + 32-token block, 8 active queries, 32-token pages "
+                             + ("stored head-major ([Hkv, 32, D] per page)" if decode["layout"] == "paged_hm"
+                                else f"({decode['layout']} layout)")
+                             + ", one layer per step over 28 layer pools"),
                 "batch": 16, "q_len": 8, "num_q_heads": 28, "num_kv_heads": 4, "head_dim": 128,
+                "kv_layout": decode["layout"],
                 "page_size": 32, "layers_cycled": LAYERS, "seqlens": decode["seqlens"],
             },
             "roofline": decode["roofline"],
             "cpu_baseline": cpu,
             "extra": {
                 "decode": {k: decode[k] for k in ("bytes_per_step", "flops_per_step", "tflops",
-                                                  "us_per_model_step_28_layers")},
+                                                  "us_per_model_step_28_layers", "layout",
+                                                  "us_per_step_token_major_pages", "ceiling") if k in decode},
                 **extra,
             },
         }

@@ -70,6 +70,7 @@ class KVAttnDesc(ctypes.Structure):
 ATTN_NO_DECODE_KERNEL = 1
 ATTN_ALL_HEADS_DECODE = 2
 ATTN_CACHE_WRITE_KERNEL = 4
+ATTN_BALANCED_SPLITS = 8
 
 KV_ATTN_SCRATCH_BYTES = 48 * 1024 * 1024  # FDLLM_KV_ATTN_SCRATCH_BYTES
 

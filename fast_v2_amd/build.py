@@ -1,9 +1,12 @@
 """Build libfdllm_hip.so (gfx950 only) in-tree with hipcc.
 
-    python -m fast_v2_amd.build            # compile if any source is newer
-    python -m fast_v2_amd.build --force    # always compile
+    python -m fast_v2_amd.build              # compile if any source is newer
+    python -m fast_v2_amd.build --force      # always compile
+    python -m fast_v2_amd.build --timeline   # also the instrumented profiling build
 
-The library lands in fast_v2_amd/lib/ so it travels with the source tree.
+The libraries land in fast_v2_amd/lib/ so they travel with the source tree:
+libfdllm_hip.so (the operators), libfdllm_probes.so (the measurement probes bench.py
+times the calls against) and, on request, libfdllm_hip_timeline.so.
 """
 from __future__ import annotations
 
@@ -20,13 +23,17 @@ CSRC = PKG_DIR / "csrc"
 LIB_DIR = PKG_DIR / "lib"
 LIB_PATH = LIB_DIR / "libfdllm_hip.so"
 # The same sources with FDLLM_TIMELINE: the split decode kernel also writes per-workgroup
-# phase stamps (fast_v2_amd.timeline reads them). A profiling build, never loaded by
-# default.
+# phase stamps (fast_v2_amd.timeline reads them). A profiling build, built on request and
+# never loaded by default.
 TIMELINE_LIB_PATH = LIB_DIR / "libfdllm_hip_timeline.so"
+PROBES_LIB_PATH = LIB_DIR / "libfdllm_probes.so"
 HEADER = REPO_DIR / "include" / "fdllm_hip.h"
+PROBES_HEADER = REPO_DIR / "include" / "fdllm_probes.h"
 
 SOURCES = [CSRC / "gather_rmsnorm.hip", CSRC / "block_attn.hip", CSRC / "rope_kv.hip", CSRC / "sampler.hip"]
 DEPS = SOURCES + [CSRC / "fdllm_common.h", HEADER]
+PROBES_SOURCES = [CSRC / "probes.hip"]
+PROBES_DEPS = PROBES_SOURCES + [PROBES_HEADER]
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [
@@ -55,28 +62,35 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found (looked at $HIPCC, PATH and /opt/rocm/bin/hipcc)")
 
 
-def needs_build() -> bool:
-    if not LIB_PATH.exists():
+def _stale(path: Path, deps) -> bool:
+    if not path.exists():
         return True
-    built = LIB_PATH.stat().st_mtime
-    return any(p.stat().st_mtime > built for p in DEPS)
+    built = path.stat().st_mtime
+    return any(p.stat().st_mtime > built for p in deps)
 
 
-def build(force: bool = True, verbose: bool = False, timeline: bool = True) -> Path:
-    """Compile every HIP source into one shared library (and, with ``timeline``, the
-    instrumented profiling build beside it, compiled concurrently); returns the path
-    of the production library."""
-    if not force and not needs_build():
+def needs_build(timeline: bool = False) -> bool:
+    """True if the operator or probe library (and, with ``timeline``, the instrumented
+    build) is missing or older than one of its sources."""
+    return (_stale(LIB_PATH, DEPS) or _stale(PROBES_LIB_PATH, PROBES_DEPS)
+            or (timeline and _stale(TIMELINE_LIB_PATH, DEPS)))
+
+
+def build(force: bool = True, verbose: bool = False, timeline: bool = False) -> Path:
+    """Compile every HIP source into the operator library and the probes library (and,
+    with ``timeline``, the instrumented profiling build), concurrently; returns the path
+    of the operator library."""
+    if not force and not needs_build(timeline):
         return LIB_PATH
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    jobs = [(LIB_PATH, [])]
+    jobs = [(LIB_PATH, [], SOURCES), (PROBES_LIB_PATH, [], PROBES_SOURCES)]
     if timeline:
-        jobs.append((TIMELINE_LIB_PATH, ["-DFDLLM_TIMELINE=1"]))
+        jobs.append((TIMELINE_LIB_PATH, ["-DFDLLM_TIMELINE=1"], SOURCES))
     procs = []
-    for path, extra in jobs:
+    for path, extra, sources in jobs:
         tmp = path.with_suffix(f".so.tmp{os.getpid()}")
         cmd = [hipcc_path(), *HIPCC_FLAGS, *extra, "-I", str(REPO_DIR / "include"),
-               *[str(s) for s in SOURCES], "-o", str(tmp)]
+               *[str(s) for s in sources], "-o", str(tmp)]
         if verbose:
             print(" ".join(cmd), flush=True)
         procs.append((path, tmp, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.PIPE, text=True)))
@@ -101,9 +115,10 @@ def build(force: bool = True, verbose: bool = False, timeline: bool = True) -> P
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--force", action="store_true")
+    ap.add_argument("--timeline", action="store_true", help="also build the instrumented profiling library")
     ap.add_argument("-v", "--verbose", action="store_true")
     args = ap.parse_args()
-    path = build(force=args.force or needs_build(), verbose=args.verbose)
+    path = build(force=args.force or needs_build(args.timeline), verbose=args.verbose, timeline=args.timeline)
     print(path)
     return 0
 

@@ -217,7 +217,7 @@ __device__ __forceinline__ SeqInfo seq_info(const AttnParams& p, const Lead& ld,
   const int row0 = rb * p.rows_per_wg;
   const int row_last = min(p.R, row0 + p.rows_per_wg) - 1;  // limits grow with t
   si.kv_end = max(0, row_key_limit(p, seqlen, si.qs, row_last / p.G));
-  si.n_act = (si.kv_end + p.chunk - 1) / p.chunk;
+  si.n_act = p.chunk > 0 ? (si.kv_end + p.chunk - 1) / p.chunk : 1;
   return si;
 }
 
@@ -1354,6 +1354,499 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   merge_splits_n<F16>(p, b, kvh, slot0, n_act, tid, 512);
   if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
   FDLLM_STAMP(5, __builtin_amdgcn_s_memrealtime());  // merge written (last arrival)
+}
+
+// ---------------------------------------------------------------------------
+// Balanced split-KV decode (opt-in, FDLLM_ATTN_BALANCED_SPLITS): the keys of all sequences
+// of one KV head, in quads of four 32-key tiles, are dealt to the S slots of the head as
+// equal runs of quads regardless of where one sequence ends and the next begins, so every
+// workgroup streams the same number of bytes (to one quad) whatever the mix of lengths.
+//   * Quads. Sequence b holds Q_b = max(1, ceil(tiles_b / 4)) quads (two steps of one tile
+//     per team), at offset off_b of the head's quad list; slot s takes quads
+//     [s P / S, (s + 1) P / S) (S <= P, so no run is empty). Every piece therefore starts
+//     on an even step, so one code path with fixed stage registers runs every piece (a
+//     piece starting on an odd step, or stage registers exchanged between pieces, made
+//     the compiler drain the loads in flight at each boundary). The run crosses from one
+//     sequence into the next ("pieces"): the load pipeline goes on across the boundary
+//     (the load cursor moves to the next sequence's pages), and at the boundary the two
+//     teams merge through the LDS of the tile buffer they just finished and both start
+//     over with the next sequence's query block.
+//   * Query blocks. The query rows of the first kBalQSlots pieces are loaded together
+//     with the first tiles and kept in LDS; a later piece (a run over many short
+//     sequences) loads its block at its boundary.
+//   * Partials. Piece (s, b) owns partial slot s + b of the head: along the runs, each
+//     new piece moves to the next slot or the next sequence, so the ids are distinct,
+//     and the pieces of sequence b occupy consecutive slots from first_slot(b) + b.
+//     A piece that is the whole of its sequence writes the output rows itself.
+//   * Arrivals. No partial is stored inside the loop (a store there makes the next
+//     steps' waits for their tiles also wait for the store's acknowledgement): the first
+//     finished piece is parked in registers; after its last step the workgroup writes
+//     its pieces, waits once for the stores, adds one arrival per stored piece to that
+//     sequence's counter, and merges the sequences whose last arrival it was, side by
+//     side.
+// Measured on the bs16 7B sub-block step (head-major pages): 30.45 us against 25.25 us
+// for the per-sequence splits of kv_split_decode_kernel; a workgroup whose run crosses a
+// sequence boundary finishes its loop about 2.5 us after one that does not, which more
+// than eats the balance gained. Hence opt-in.
+// Conditions (host): batch <= 64 (one wave lane per sequence in the partition), the
+// whole page table in LDS (batch * max_pages <= kBalMaxPages) or a contiguous cache,
+// head_dim 128, at most 64 query rows per KV head.
+constexpr int kBalQSlots = 3;
+constexpr int kBalMaxPages = 4096;
+// LDS placement of the balanced decode kernel's regions (byte offsets in one arena): team
+// 0's two tile buffers, team 1's, the query blocks, the page table, the per-sequence
+// facts. (Five placements of the team buffers relative to the query blocks and the 80 KB
+// mark ran alike.)
+struct BalLds {
+  static constexpr int kTile = 2 * (32 * (128 + 8) + 32 * (128 + 16)) * 2;  // two buffers of one team
+  static constexpr int kQRow = 128 + 8;  // query row in LDS, padded: the 16 rows of one read hit distinct banks
+  static constexpr int kQBytes = kBalQSlots * 64 * kQRow * 2;
+  static constexpr int kPagesBytes = kBalMaxPages * 4;
+  static constexpr int kSmallBytes = (65 + 8 * 64) * 4;
+  static constexpr int kTeam0 = 0, kTeam1 = kTile, kQ = 2 * kTile, kPages = kQ + kQBytes, kSmall = kPages + kPagesBytes;
+  static constexpr int kBytes = kSmall + kSmallBytes;  // the regions in this order, end to end
+};
+static_assert(BalLds::kBytes <= 160 * 1024, "balanced decode LDS fits one CU");
+
+template <bool F16, bool PAGED>
+__global__ __launch_bounds__(512, 2) void kv_balanced_decode_kernel(FDLLM_LEAD_PARAMS, const AttnParams p) {
+  FDLLM_LEAD_LOCAL;
+  FDLLM_STAMP(0, __builtin_amdgcn_s_memrealtime());  // start
+  constexpr int D = 128;
+  constexpr int KT = 32;
+  constexpr int KS = D + 8;
+  constexpr int VS = D + 16;
+  constexpr int NDT = D / 16;
+  constexpr int KBUF = KT * KS;
+  constexpr int VBUF = KT * VS;
+  // One LDS arena with placed regions (BalLds): each team's two tile buffers (K then V),
+  // the query blocks, the page table and the per-sequence facts.
+  __shared__ __attribute__((aligned(16))) unsigned char smem[BalLds::kBytes];
+  uint16_t(*const sKVt)[2][KBUF + VBUF] = reinterpret_cast<uint16_t(*)[2][KBUF + VBUF]>(smem);  // unused base
+  auto sKV_of = [&](int buf, int tm) {
+    return reinterpret_cast<uint16_t*>(smem + (tm ? BalLds::kTeam1 : BalLds::kTeam0) + buf * (KBUF + VBUF) * 2);
+  };
+  (void)sKVt;
+  int* const sAllPages = reinterpret_cast<int*>(smem + BalLds::kPages);
+  uint16_t(*const sQ)[64 * BalLds::kQRow] = reinterpret_cast<uint16_t(*)[64 * BalLds::kQRow]>(smem + BalLds::kQ);
+  int* const sOff = reinterpret_cast<int*>(smem + BalLds::kSmall);  // [65] pair offset of each sequence; sOff[B] = P
+  int* const sLen = sOff + 65;     // [64] visible length
+  int* const sQs = sLen + 64;      // [64] query start
+  int* const sEnd = sQs + 64;      // [64] key bound
+  int* const sNs = sEnd + 64;      // [64] pieces of each sequence
+  int* const sFirst = sNs + 64;    // [64] first partial slot
+  int* const sArr = sFirst + 64;   // [64] sequences this workgroup stored a partial for
+  int* const sLast = sArr + 64;    // [64]
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int team = __builtin_amdgcn_readfirstlane(wave >> 2);
+  const int wt = wave & 3;
+  const int ttid = tid & 255;
+  const int l16 = lane & 15;
+  const int g = lane >> 4;
+  const int kvh = blockIdx.y;
+
+  // the whole page table, read together with the lengths
+  const int n_pt = PAGED ? ld.B * ld.max_pages : 0;
+  int pf[kBalMaxPages / 512];
+  if constexpr (PAGED) {
+#pragma unroll
+    for (int u = 0; u < kBalMaxPages / 512; ++u) {
+      const int idx = tid + 512 * u;
+      pf[u] = idx < n_pt ? ld.page_table[idx] : 0;
+    }
+  }
+  // ---- partition (every wave evaluates it; lane b holds sequence b)
+  const bool has = lane < ld.B;
+  SeqInfo sl;
+  sl.seqlen = sl.qs = sl.kv_end = 0;
+  if (has) sl = seq_info<PAGED>(p, ld, lane, 0);
+  const int tiles = (sl.kv_end + KT - 1) / KT;
+  const int quads = has ? max(1, (tiles + 3) >> 2) : 0;  // two steps of two tiles
+  const int incl = wave_incl_scan_i32(quads);
+  const int off = incl - quads;
+  const int P = __builtin_amdgcn_readlane(incl, 63);
+  const int S = min(p.n_splits, P);  // active slots, each with at least one quad
+  const int x = blockIdx.x;
+  const int slot = (p.n_splits & 7) == 0 ? (x & 7) * (p.n_splits >> 3) + (x >> 3) : x;
+  if (slot >= S) return;  // uniform
+  const int qlo = static_cast<int>(static_cast<int64_t>(slot) * P / S);
+  const int qhi = static_cast<int>(static_cast<int64_t>(slot + 1) * P / S);
+  // slot holding quad y: the largest s with floor(s P / S) <= y
+  auto slot_of = [&](int y) { return static_cast<int>((static_cast<int64_t>(y + 1) * S + P - 1) / P) - 1; };
+  if (wave == 0) {
+    if (has) {
+      sOff[lane] = 2 * off;  // in steps
+      sLen[lane] = sl.seqlen;
+      sQs[lane] = sl.qs;
+      sEnd[lane] = sl.kv_end;
+      const int s0 = slot_of(off);
+      sNs[lane] = slot_of(off + quads - 1) - s0 + 1;
+      sFirst[lane] = s0 + lane;
+    }
+    if (lane == 0) sOff[ld.B] = 2 * P;
+  }
+  const int b0 = static_cast<int>(__builtin_ctzll(__builtin_amdgcn_ballot_w64(has && off <= qlo && qlo < incl)));
+  const int b_last = static_cast<int>(__builtin_ctzll(__builtin_amdgcn_ballot_w64(has && off < qhi && qhi <= incl)));
+  const int lo = 2 * qlo, hi = 2 * qhi;  // the run in steps (pairs of tiles)
+  FDLLM_STAMP(1, __builtin_amdgcn_s_memrealtime());  // partition known
+  if constexpr (PAGED) {
+#pragma unroll
+    for (int u = 0; u < kBalMaxPages / 512; ++u) {
+      const int idx = tid + 512 * u;
+      if (idx < n_pt) sAllPages[idx] = pf[u];
+    }
+  }
+  __syncthreads();  // page table and sequence facts visible
+  const int n = hi - lo;  // steps of this workgroup (even)
+
+  f32x4 acc[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
+
+  // chunk c = ttid + 256 i of a tile: key c / 16, 16-byte column c % 16
+  const int krow_bytes = static_cast<int>(p.k_ss) * 2;
+  const int vrow_bytes = static_cast<int>(p.v_ss) * 2;
+  int koff[2], voff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = ttid + 256 * i;
+    koff[i] = (c >> 4) * krow_bytes + (c & 15) * 16;
+    voff[i] = (c >> 4) * vrow_bytes + (c & 15) * 16;
+  }
+  const uint16_t* kbase = p.k + kvh * p.k_sh;
+  const uint16_t* vbase = p.v + kvh * p.v_sh;
+  struct Stage {
+    u32x4 k[2];
+    u32x4 v[2];
+  };
+  Stage st0, st1;
+
+  // load cursor: the sequence of the pair being loaded (moves forward only)
+  int lb = b0;
+  int l_off = sOff[lb];
+  int l_end = sOff[lb + 1];
+  int l_kv = sEnd[lb];
+  auto load_tile = [&](Stage& sg, int j) {
+    const int gq = lo + j;
+    if (gq < hi) {
+      while (gq >= l_end) {  // uniform; at most once per step for sequences of >= 1 pair
+        ++lb;
+        l_off = l_end;
+        l_end = sOff[lb + 1];
+        l_kv = sEnd[lb];
+      }
+    }
+    const int kb = (min(gq, hi - 1) - l_off) * 64 + 32 * team;
+    const int valid = __builtin_amdgcn_readfirstlane(gq < hi ? max(0, min(KT, l_kv - kb)) : 0);
+    int64_t koffs, voffs;
+    if constexpr (PAGED) {
+      const int page = __builtin_amdgcn_readfirstlane(
+          sAllPages[lb * p.max_pages + min(kb >> p.page_shift, p.max_pages - 1)]);
+      const int slot0 = kb & (p.page_size - 1);
+      koffs = static_cast<int64_t>(page) * p.k_sp + slot0 * p.k_ss;
+      voffs = static_cast<int64_t>(page) * p.v_sp + slot0 * p.v_ss;
+    } else {
+      koffs = static_cast<int64_t>(lb) * p.k_sp + static_cast<int64_t>(kb) * p.k_ss;
+      voffs = static_cast<int64_t>(lb) * p.v_sp + static_cast<int64_t>(kb) * p.v_ss;
+    }
+    const __amdgpu_buffer_rsrc_t kr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(kbase + koffs), 0, valid * krow_bytes, kBufferFlags);
+    const __amdgpu_buffer_rsrc_t vr =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(vbase + voffs), 0, valid * vrow_bytes, kBufferFlags);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      sg.k[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[i], 0, kSlcNt));
+      sg.v[i] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, kSlcNt));
+    }
+  };
+  auto store_tile = [&](const Stage& sg, int buf) {
+    uint16_t* sk = sKV_of(buf, team);
+    uint16_t* sv = sk + KBUF;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = ttid + 256 * i;
+      *reinterpret_cast<u32x4*>(&sk[(c >> 4) * KS + (c & 15) * 8]) = sg.k[i];
+      *reinterpret_cast<u32x4*>(&sv[(c >> 4) * VS + (c & 15) * 8]) = sg.v[i];
+    }
+  };
+  // query rows of sequence b: chunk c = tid + 512 i is row c / 16 (padding rows repeat
+  // the last row: finite, never written), 16-byte column c % 16
+  auto q_chunk = [&](int b, int i) {
+    const int c = tid + 512 * i;
+    const int rc = min(c >> 4, p.R - 1);
+    const int t = rc / p.G;
+    const int hh = rc - t * p.G;
+    return *reinterpret_cast<const u32x4*>(p.q + b * p.q_sb + t * p.q_ss + (kvh * p.G + hh) * p.q_sh + (c & 15) * 8);
+  };
+  auto q_store = [&](int qslot, int i, const u32x4& v) {
+    const int c = tid + 512 * i;
+    *reinterpret_cast<u32x4*>(&sQ[qslot][(c >> 4) * BalLds::kQRow + (c & 15) * 8]) = v;
+  };
+
+  load_tile(st0, 0);
+  // query blocks of the first pieces (a piece past b_last loads b_last's block again)
+  u32x4 qpre[kBalQSlots][2];
+#pragma unroll
+  for (int u = 0; u < kBalQSlots; ++u)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) qpre[u][i] = q_chunk(min(b0 + u, b_last), i);
+  load_tile(st1, 1);
+
+  // compute cursor: the sequence of the piece being computed
+  int cb = b0;
+  int piece = 0;
+  int narr = 0;  // partials stored by this workgroup (uniform)
+  u32x4 qf[4];
+  int lim = 0, lim_min = 0;
+  const float rescale_thr = 8.f / p.scale_log2;
+
+  auto compute_tile = [&](int buf, int kb) {
+    const uint16_t* sk = sKV_of(buf, team);
+    const uint16_t* sv = sk + KBUF;
+    f32x4 s[2] = {f32x4{0.f, 0.f, 0.f, 0.f}, f32x4{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+      for (int st2 = 0; st2 < 2; ++st2) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(&sk[(st2 * 16 + l16) * KS + ks * 32 + g * 8]);
+        s[st2] = mfma16x16x32<F16>(kf, qf[ks], s[st2]);
+      }
+    if (!(kb + KT <= lim_min)) {  // wave-uniform: some row of the wave sees only part of the tile
+#pragma unroll
+      for (int st2 = 0; st2 < 2; ++st2)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (kb + st2 * 16 + g * 4 + j >= lim) s[st2][j] = -INFINITY;
+    }
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int st2 = 0; st2 < 2; ++st2)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) tmax = fmaxf(tmax, s[st2][j]);
+    tmax = group4_allreduce_max(tmax);
+    if (__builtin_amdgcn_ballot_w64(tmax > m_run + rescale_thr) != 0) {
+      const float m_new = fmaxf(m_run, tmax);
+      const float alpha = m_run == -INFINITY ? 0.f : fast_exp2((m_run - m_new) * p.scale_log2);
+      l_run *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) acc[dt] *= alpha;
+      m_run = m_new;
+    }
+    const float mc = m_run == -INFINITY ? 0.f : m_run * p.scale_log2;
+    float lsum = 0.f;
+#pragma unroll
+    for (int st2 = 0; st2 < 2; ++st2)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float e = fast_exp2(fmaf(s[st2][j], p.scale_log2, -mc));
+        s[st2][j] = e;
+        lsum += e;
+      }
+    l_run += lsum;
+    u32x4 pk;
+    pk[0] = pack2<F16>(s[0][0], s[0][1]);
+    pk[1] = pack2<F16>(s[0][2], s[0][3]);
+    pk[2] = pack2<F16>(s[1][0], s[1][1]);
+    pk[3] = pack2<F16>(s[1][2], s[1][3]);
+    const int vrow = 4 * g + (l16 >> 2);
+    const int vcol = 4 * (l16 & 3);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) {
+      const s16x4 lo4 = lds_read_tr16(&sv[vrow * VS + vcol + dt * 16]);
+      const s16x4 hi4 = lds_read_tr16(&sv[(vrow + 16) * VS + vcol + dt * 16]);
+      const u32x2 lo2 = __builtin_bit_cast(u32x2, lo4);
+      const u32x2 hi2 = __builtin_bit_cast(u32x2, hi4);
+      acc[dt] = mfma16x16x32<F16>(u32x4{lo2[0], lo2[1], hi2[0], hi2[1]}, pk, acc[dt]);
+    }
+  };
+
+  // Output rows (a piece that is its whole sequence) or the partial of piece (slot, b),
+  // from team 0's merged state.
+  const int r = wt * 16 + l16;  // this lane's query row
+  auto emit = [&](int b, const f32x4 (&a)[NDT], float m, float l) {
+    if (team != 0 || r >= p.R) return;  // padding rows are never read
+    if (sNs[b] <= 1) {
+      const int t = r / p.G;
+      const int hh = r - t * p.G;
+      const float inv = l > 0.f ? 1.f / l : 0.f;
+      uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const f32x4 o = a[dt] * inv;
+        *reinterpret_cast<u32x2*>(orow + dt * 16 + g * 4) = u32x2{pack2<F16>(o[0], o[1]), pack2<F16>(o[2], o[3])};
+      }
+      return;
+    }
+    const int64_t pslot = static_cast<int64_t>(kvh) * (p.n_splits + p.B) + slot + b;
+    const auto orsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_o + pslot * 64 * D, 0, 64 * D * 4, kBufferFlags);
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, a[dt]), orsrc, (r * D + dt * 16 + g * 4) * 4, 0,
+                                             kSc1);
+    if (g == 0) {
+      const auto mrsrc = __builtin_amdgcn_make_buffer_rsrc(p.ws_ml + pslot * 64, 0, 64 * 8, kBufferFlags);
+      __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, make_float2(m, l)), mrsrc, r * 8, 0, kSc1);
+    }
+  };
+  // A piece that ends before the run does is parked in registers (one such piece) and
+  // written after the loop: stores issued inside the loop would make the next steps'
+  // waits for their tiles also wait for the stores' acknowledgement.
+  f32x4 hacc[NDT];
+  float hm = -INFINITY, hl = 0.f;
+  int hb = -1;  // sequence of the parked piece (uniform), -1: none
+
+  // End of a piece (workgroup-uniform): the teams merge through buffer `buf` of both
+  // teams (idle until the tile two steps on is stored there, after the next barrier),
+  // team 0 parks or writes the result, and both teams start over.
+  constexpr int XS = NDT * 4 + 2;
+  static_assert(2 * 64 * XS * 4 <= (KBUF + VBUF) * 2, "half of the team merge fits one buffer of one team");
+  // waves 0-1 of team 1 hand over through team 0's buffer `buf`, waves 2-3 through team 1's
+  float* const xwave = reinterpret_cast<float*>(sKV_of(0, wt >> 1)) + ((wt & 1) * 64 + lane) * XS;
+  auto finalize = [&](int buf, bool last_piece) {
+    float* xs_base = xwave + buf * (KBUF + VBUF) / 2;  // (KBUF + VBUF) 16-bit words = half as many floats
+    lds_barrier();  // both teams are done with the tiles in `buf`
+    if (team == 1) {
+      float* xs = xs_base;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) xs[dt * 4 + j] = acc[dt][j];
+      xs[NDT * 4] = m_run;
+      xs[NDT * 4 + 1] = l_run;
+    }
+    lds_barrier();
+    if (team == 0) {
+      const float* xs = xs_base;
+      const float m1 = xs[NDT * 4];
+      const float l1 = xs[NDT * 4 + 1];
+      const float m_new = fmaxf(m_run, m1);
+      const float a0 = m_run == -INFINITY ? 0.f : fast_exp2((m_run - m_new) * p.scale_log2);
+      const float a1 = m1 == -INFINITY ? 0.f : fast_exp2((m1 - m_new) * p.scale_log2);
+      l_run = l_run * a0 + l1 * a1;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[dt][j] = acc[dt][j] * a0 + xs[dt * 4 + j] * a1;
+      m_run = m_new;
+      l_run = group4_allreduce_sum(l_run);
+    }
+    if (last_piece) {
+      emit(cb, acc, m_run, l_run);
+    } else if (hb < 0) {
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) hacc[dt] = acc[dt];
+      hm = m_run;
+      hl = l_run;
+      hb = cb;
+    } else {
+      emit(cb, acc, m_run, l_run);  // a run over several short sequences: written now
+    }
+    if (sNs[cb] > 1) {
+      if (tid == 0) sArr[narr] = cb;
+      ++narr;
+    }
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_run = -INFINITY;
+    l_run = 0.f;
+  };
+
+  // One step: the pair of tiles of step j into LDS, the loads of step j + 2 issued,
+  // then this team's tile of step j (the piece's keys start at pair c_off, end at c_kv).
+  auto step = [&](Stage& sg, int j, int c_off, int c_kv) {
+    store_tile(sg, j & 1);
+    lds_barrier();
+    load_tile(sg, j + 2);
+    const int kb = (lo + j - c_off) * 64 + 32 * team;
+    if (kb < c_kv) compute_tile(j & 1, kb);  // wave-uniform
+  };
+  // Steps [j, e) of one piece (j and e even): even steps' tiles are in st0, odd steps' in
+  // st1, on every path (a stage register set copied while its loads are in flight would
+  // make the copy wait for them, and a piece starting on an odd step would leave the
+  // compiler's wait counts at the piece loop conservative: full drains).
+  auto run_steps = [&](int& j, int e, int c_off, int c_kv) {
+    for (; j < e; j += 2) {
+      step(st0, j, c_off, c_kv);
+      step(st1, j + 1, c_off, c_kv);
+    }
+  };
+
+  // The query blocks of the first pieces into LDS: their wait also covers the first
+  // tile (loaded before them); the second tile stays in flight.
+#pragma unroll
+  for (int u = 0; u < kBalQSlots; ++u)
+#pragma unroll
+    for (int i = 0; i < 2; ++i) q_store(u, i, qpre[u][i]);
+  lds_barrier();
+  FDLLM_STAMP(2, __builtin_amdgcn_s_memrealtime());  // first tile and query blocks landed
+  int j = 0;  // next step (pair of the run)
+  while (true) {  // one iteration per piece (workgroup-uniform)
+    const int c_off = sOff[cb];
+    const int e = min(sOff[cb + 1], hi) - lo;  // the piece's steps end before e
+    const int c_kv = sEnd[cb];
+    {
+      const uint16_t* qrow = &sQ[piece % kBalQSlots][r * BalLds::kQRow];
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qrow + ks * 32 + g * 8);
+      const int rc = min(r, p.R - 1);  // padding rows take a valid row's limit
+      lim = min(row_key_limit(p, sLen[cb], sQs[cb], rc / p.G), c_kv);
+      lim_min = __builtin_amdgcn_readfirstlane(-static_cast<int>(wave_allreduce_max(-static_cast<float>(lim))));
+    }
+    run_steps(j, e, c_off, c_kv);
+    finalize((j - 1) & 1, j == n);
+    if (j == n) break;
+    if (piece == 0) FDLLM_STAMP(7, __builtin_amdgcn_s_memrealtime());  // first boundary passed
+    ++cb;
+    ++piece;
+    if (piece >= kBalQSlots) {
+      // a run over many short sequences: this piece's query block loads now into the
+      // slot of piece - kBalQSlots (finished)
+#pragma unroll
+      for (int i = 0; i < 2; ++i) q_store(piece % kBalQSlots, i, q_chunk(cb, i));
+      lds_barrier();
+    }
+  }
+  if (hb >= 0) emit(hb, hacc, hm, hl);  // uniform: the parked piece
+  FDLLM_STAMP(3, __builtin_amdgcn_s_memrealtime());  // key loop done (every piece finalized)
+  FDLLM_STAMP(6, (static_cast<uint64_t>(b0) << 48) | (static_cast<uint64_t>(b_last - b0 + 1) << 32) |
+                     static_cast<uint64_t>(2 * n));
+  if (narr == 0) return;  // uniform: every piece wrote its output rows
+  // Publish the stored partials (device-coherent stores, acknowledged), then count one
+  // arrival per stored piece; the workgroup that brings a sequence's counter to its
+  // piece count merges that sequence's partials.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (tid < narr) {
+    const int b = sArr[tid];
+    sLast[tid] = __hip_atomic_fetch_add(&p.ws_cnt[b * p.Hkv + kvh], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 sNs[b] - 1;
+  }
+  __syncthreads();
+  FDLLM_STAMP(4, __builtin_amdgcn_s_memrealtime());  // arrivals counted
+  // the sequences this workgroup merges, run side by side (one group of threads each:
+  // the merge is bound by its loads' round trip, not by the threads)
+  int nm = 0;
+  for (int i = 0; i < narr; ++i) nm += sLast[i] ? 1 : 0;  // uniform
+  if (nm == 0) return;
+  const int groups = min(nm, 4);
+  const int gsize = 512 / groups;  // 512, 256 or 128 threads (3 merges: 128 each, one group idle)
+  const int grp = tid / (groups == 3 ? 128 : gsize);
+  for (int i = 0, k = 0; i < narr; ++i) {
+    if (!sLast[i]) continue;  // uniform
+    if (k % groups == grp) {
+      const int b = sArr[i];
+      const int64_t slot0 = static_cast<int64_t>(kvh) * (p.n_splits + p.B) + sFirst[b];
+      const int gtid = tid - grp * (groups == 3 ? 128 : gsize);
+      merge_splits_n<F16>(p, b, kvh, slot0, sNs[b], gtid, groups == 3 ? 128 : gsize);
+      if (gtid == 0) __hip_atomic_store(&p.ws_cnt[b * p.Hkv + kvh], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    ++k;
+  }
+  FDLLM_STAMP(5, __builtin_amdgcn_s_memrealtime());  // merges written
 }
 
 
@@ -2850,7 +3343,8 @@ enum PlanKind {
   kPlanSplitDecode = 2,
   kPlanPrefill = 3,
   kPlanSplitPrefill = 4,
-  kPlanF32 = 5
+  kPlanF32 = 5,
+  kPlanBalancedDecode = 6
 };
 
 struct Plan {
@@ -2941,6 +3435,21 @@ int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
       pl->n_rb = 1;
       int64_t slots;  // partial slots per KV head
       bool split_possible;
+      const bool pages_fit = d->page_table == nullptr || B * d->max_pages <= kBalMaxPages;
+      if (d->kv_split == 0 && B <= kBalancedMaxBatch && pages_fit && (d->flags & FDLLM_ATTN_BALANCED_SPLITS)) {
+        // pairs of 32-key tiles dealt evenly over S slots per KV head (S * Hkv ~ one
+        // workgroup per CU, S a multiple of 8 for the XCD-major slot order); partial
+        // slots S + batch per head (piece (s, b) owns slot s + b)
+        pl->kind = kPlanBalancedDecode;
+        pl->chunk = 0;
+        const int64_t s8 = std::max<int64_t>(8, (kSplitTargetWG / hkv + 7) / 8 * 8);
+        pl->n_splits = static_cast<int>(s8);
+        const int64_t pslots = s8 + B;
+        FDLLM_CHECK_ARG(pslots * hkv < (int64_t{1} << 31) / 64, "fdllm_kv_attn: too many split slots");
+        pl->ws_o_bytes = static_cast<size_t>(pslots) * hkv * 64 * d->head_dim * sizeof(float);
+        pl->ws_ml_bytes = static_cast<size_t>(pslots) * hkv * 64 * sizeof(float2);
+        return FDLLM_OK;
+      }
       if (d->kv_split == 0 && B <= kBalancedMaxBatch) {
         pl->chunk = 0;
         slots = std::max<int64_t>((kSplitTargetWG + hkv - 1) / hkv, B * min_splits);
@@ -3336,7 +3845,12 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
   // with FDLLM_ATTN_CACHE_WRITE_KERNEL) as a kernel of its own before the attention, at
   // q_start[b] + t (seqlens[b] - q_len + t). On the 4 x 4096-token prefill, timed in
   // rotation: 473-475 us in-kernel against 479-480 us with the copy kernel.
-  const bool fuse_write = p.kn != nullptr && !(d->flags & FDLLM_ATTN_CACHE_WRITE_KERNEL) &&
+  // The prefill kernels read every key at or past the query start from the new rows,
+  // which is exact only when no visible key lies past the last new row. Without q_start
+  // that holds by construction (query start = visible length - q_len); an explicit
+  // q_start may leave visible cache rows past q_start + q_len, so such calls take the
+  // copy kernel, which stores the rows before the attention reads the cache.
+  const bool fuse_write = p.kn != nullptr && p.q_start == nullptr && !(d->flags & FDLLM_ATTN_CACHE_WRITE_KERNEL) &&
                           (pl.kind == kPlanPrefill || pl.kind == kPlanSplitPrefill);
   if (p.kn != nullptr && !fuse_write) {
     KVWriteArgs a;
@@ -3366,6 +3880,18 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
     a.D = d->head_dim;
     const int64_t n = static_cast<int64_t>(a.B) * a.T * a.Hkv * (a.D / 8);
     kv_write_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(a);
+  }
+  if (pl.kind == kPlanBalancedDecode) {
+    const bool paged = p.page_table != nullptr;
+    const dim3 grid(pl.n_splits, d->num_kv_heads);
+    if (f16) {
+      if (paged) kv_balanced_decode_kernel<true, true><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+      else kv_balanced_decode_kernel<true, false><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+    } else {
+      if (paged) kv_balanced_decode_kernel<false, true><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+      else kv_balanced_decode_kernel<false, false><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+    }
+    FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }
   if (pl.kind == kPlanSplitDecode) {
     const bool paged = p.page_table != nullptr;

@@ -160,16 +160,23 @@ struct GatherArgs {
 // The arguments the index load and the row address need come first, as scalars: with
 // kernel-argument preloading they arrive in SGPRs at wave launch, so the index load
 // is the first memory access (the rest of the arguments load beside it).
+// Rows (waves) per workgroup of the vector path.
+#ifndef FDLLM_GATHER_ROWS_PER_WG
+#define FDLLM_GATHER_ROWS_PER_WG 4
+#endif
+constexpr int kGatherRows = FDLLM_GATHER_ROWS_PER_WG;
+
 template <typename T, int WK, bool CAST, bool GATHERED, int VPL>
-__global__ __launch_bounds__(256) void gather_rmsnorm_vec_kernel(const int64_t* idx, int64_t is_b,
+__global__ __launch_bounds__(64 * kGatherRows) void gather_rmsnorm_vec_kernel(const int64_t* idx, int64_t is_b,
                                                                  const void* hidden, int64_t hs_b, int64_t hs_s,
                                                                  int T_rows, int S_rows, const GatherArgs a) {
   constexpr int N = Vec16<T>::N;
   const int lane = threadIdx.x & (kWave - 1);
-  // grid (ceil(T / 4), B): four rows of one sequence per workgroup, no division; the row
-  // is wave-uniform, so its index, bounds check and addresses live in scalar registers
+  // grid (ceil(T / kGatherRows), B): kGatherRows rows of one sequence per workgroup, no
+  // division; the row is wave-uniform, so its index, bounds check and addresses live in
+  // scalar registers
   const int b = blockIdx.y;
-  const int t = static_cast<int>(blockIdx.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t = static_cast<int>(blockIdx.x) * kGatherRows + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   if (t >= T_rows) return;
   const int64_t src = idx[b * is_b + t];
   const int nvec = a.H / N;
@@ -342,7 +349,7 @@ bool launch_gather_vec(const GatherArgs& a, dim3 grid, hipStream_t stream) {
   switch (vpl) {
 #define FDLLM_VPL_CASE(n)                                                                  \
   case n:                                                                                  \
-    gather_rmsnorm_vec_kernel<T, WK, CAST, GATHERED, n><<<grid, dim3(256), 0, stream>>>(  \
+    gather_rmsnorm_vec_kernel<T, WK, CAST, GATHERED, n><<<grid, dim3(64 * kGatherRows), 0, stream>>>(  \
         a.idx, a.is_b, a.hidden, a.hs_b, a.hs_s, a.T, a.S, a);                              \
     return true;
     FDLLM_VPL_CASE(1)
@@ -380,7 +387,7 @@ int launch_gather(const GatherArgs& a, bool vec, hipStream_t stream) {
   const int64_t rows = static_cast<int64_t>(a.B) * a.T;
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
   if (vec && a.B <= 65535) {
-    const dim3 vgrid(static_cast<unsigned>((a.T + 3) / 4), static_cast<unsigned>(a.B));
+    const dim3 vgrid(static_cast<unsigned>((a.T + kGatherRows - 1) / kGatherRows), static_cast<unsigned>(a.B));
     bool done;
     if (a.mode == FDLLM_NORM_PLAIN) {
       done = launch_gather_vec_out<T, kWNone, false>(a, vgrid, stream);

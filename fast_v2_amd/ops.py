@@ -271,6 +271,7 @@ def block_attn(
     k_new: Optional[torch.Tensor] = None,
     v_new: Optional[torch.Tensor] = None,
     cache_write_kernel: bool = False,
+    balanced_splits: bool = False,
 ) -> torch.Tensor:
     """Attention of BSHD queries over a (paged) BSHD KV cache.
 
@@ -288,6 +289,9 @@ def block_attn(
     as part of the call, before any key is read (StaticKVCache.update followed by the
     attention, static_kv_cache.py:132-160): inside the prefill kernels, otherwise (and
     with cache_write_kernel=True) by a copy kernel ahead of the attention (same results).
+    balanced_splits=True deals all sequences' keys evenly over the sub-block decode
+    workgroups (runs that cross sequence boundaries) instead of splitting each sequence
+    on its own.
     """
     if q.dim() != 4 or k_cache.dim() != 4 or v_cache.dim() != 4:
         raise RuntimeError("block_attn: q, k_cache and v_cache must be 4-D (BSHD)")
@@ -345,7 +349,8 @@ def block_attn(
                       mask_block, q_start, page_table, page_size, kv_split,
                       (0 if decode_kernel else _ffi.ATTN_NO_DECODE_KERNEL)
                       | (_ffi.ATTN_ALL_HEADS_DECODE if all_heads_decode else 0)
-                      | (_ffi.ATTN_CACHE_WRITE_KERNEL if cache_write_kernel else 0), k_new, v_new)
+                      | (_ffi.ATTN_CACHE_WRITE_KERNEL if cache_write_kernel else 0)
+                      | (_ffi.ATTN_BALANCED_SPLITS if balanced_splits else 0), k_new, v_new)
     L = _ffi.lib()
     need = ctypes.c_size_t(0)
     _ffi.check(L.fdllm_kv_attn_workspace_size(ctypes.byref(desc), ctypes.byref(need)),

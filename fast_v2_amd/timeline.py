@@ -3,7 +3,8 @@ sequences, 8 active queries, 28 query / 4 KV heads, head_dim 128, 32-token pages
 prefix lengths of workloads.kv_decode_paged(seed=0)).
 
 It loads the instrumented library lib/libfdllm_hip_timeline.so (the production sources
-built with FDLLM_TIMELINE, beside lib/libfdllm_hip.so), in which thread 0 of each
+built with FDLLM_TIMELINE by `python -m fast_v2_amd.build --timeline`, beside
+lib/libfdllm_hip.so; refused when it is older than a source), in which thread 0 of each
 workgroup of kv_split_decode_kernel writes the device's 100 MHz real-time clock at the
 end of each phase:
 
@@ -81,13 +82,29 @@ def main(argv=None) -> int:
     ap.add_argument("--calls", type=int, default=56)
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--full-block", action="store_true", help="all 32 block queries active")
+    ap.add_argument("--token-major", action="store_true",
+                    help="pages stored [page_size, Hkv, D] (default: head-major [Hkv, page_size, D])")
+    ap.add_argument("--balanced-splits", action="store_true",
+                    help="deal all sequences' keys evenly over the workgroups (runs across sequence boundaries)")
+    ap.add_argument("--dump", default=None, help="also save every call's raw stamps [calls, workgroups, 8] (.npy)")
+    ap.add_argument("--lib", default=None, help="instrumented library to load (default: lib/libfdllm_hip_timeline.so)")
+    ap.add_argument("--prefix", type=int, default=None, help="every sequence's cached prefix (default: U{1024..4096})")
+    ap.add_argument("--back-to-back", type=int, default=0, metavar="N",
+                    help="time each sample as the last of N calls replayed back to back from a HIP graph "
+                         "(the benchmark's regime) instead of one call from an idle GPU")
     args = ap.parse_args(argv)
     if "fast_v2_amd._ffi" in sys.modules:
         raise RuntimeError("fast_v2_amd.timeline must load the instrumented library before anything else loads "
                            "the production one: run it as its own process")
-    if not TIMELINE_LIB.exists():
-        raise RuntimeError(f"{TIMELINE_LIB} is not built (python -m fast_v2_amd.build --force)")
-    os.environ["FDLLM_HIP_LIB"] = str(TIMELINE_LIB)
+    lib_path = Path(args.lib) if args.lib else TIMELINE_LIB
+    if args.lib is None:
+        from . import build as _build
+        if _build._stale(TIMELINE_LIB, _build.DEPS):  # missing, or older than a source
+            raise RuntimeError(f"{lib_path} is missing or older than the sources: "
+                               "python -m fast_v2_amd.build --timeline")
+    if not lib_path.exists():
+        raise RuntimeError(f"{lib_path} does not exist")
+    os.environ["FDLLM_HIP_LIB"] = str(lib_path)
     import numpy as np
     import torch
 
@@ -99,10 +116,13 @@ def main(argv=None) -> int:
     attach.restype = ctypes.c_int
 
     dev = torch.device("cuda", 0)
-    wl = workloads.kv_decode_paged(seed=0, active=32 if args.full_block else 8)
+    lens = {} if args.prefix is None else dict(min_prefix=args.prefix, max_prefix=args.prefix)
+    wl = workloads.kv_decode_paged(seed=0, active=32 if args.full_block else 8, head_major=not args.token_major, **lens)
     layers = args.layers
     gen = torch.Generator(device=dev).manual_seed(1)
     kp = torch.empty((layers,) + tuple(wl.k_pool.shape), dtype=wl.k_pool.dtype, device=dev)
+    if not args.token_major:  # the same storage order as the pool: [layers, pages, Hkv, page_size, D]
+        kp = kp.transpose(-3, -2).contiguous().transpose(-3, -2)
     vp = torch.empty_like(kp)
     kp[0].copy_(wl.k_pool)
     vp[0].copy_(wl.v_pool)
@@ -113,28 +133,51 @@ def main(argv=None) -> int:
     out = torch.empty_like(q)
 
     def call(layer):
-        ops.block_attn(q, kp[layer], vp[layer], sl, wl.scale, page_table=pt, page_size=wl.page_size, out=out)
+        ops.block_attn(q, kp[layer], vp[layer], sl, wl.scale, page_table=pt, page_size=wl.page_size, out=out,
+                       balanced_splits=args.balanced_splits)
 
     for i in range(2 * layers):
         call(i % layers)
     torch.cuda.synchronize()
     stamps = torch.zeros(MAX_WORKGROUPS * STAMPS, dtype=torch.int64, device=dev)
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    per_call, event_us = [], []
+    per_call, event_us, dumps = [], [], []
     if attach(ctypes.c_void_p(stamps.data_ptr())) != 0:
         raise RuntimeError("fdllm_timeline_attach failed")
     try:
+        graph = None
+        if args.back_to_back > 0:
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                for i in range(2):
+                    call(i % layers)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph, stream=s):
+                for i in range(args.back_to_back):
+                    call(i % layers)
+            torch.cuda.synchronize()
         for c in range(args.calls):
             stamps.zero_()
             torch.cuda.synchronize()
             start.record()
-            call(c % layers)
+            if graph is not None:
+                graph.replay()  # every call overwrites the stamps: the last call's remain
+            else:
+                call(c % layers)
             end.record()
             torch.cuda.synchronize()
             event_us.append(start.elapsed_time(end) * 1e3)
-            per_call.append(analyse(stamps.view(-1, STAMPS).cpu().numpy()))
+            raw = stamps.view(-1, STAMPS).cpu().numpy()
+            per_call.append(analyse(raw))
+            if args.dump:
+                dumps.append(raw[: 4096].copy())
     finally:
         attach(None)
+
+    if args.dump:
+        np.save(args.dump, np.stack(dumps))
 
     def med(key, j=None):
         vals = [r[key] if j is None else r[key][j] for r in per_call]

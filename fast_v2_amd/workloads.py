@@ -90,10 +90,13 @@ def kv_decode_paged(seed: int = 0, batch: int = 16, num_q_heads: int = 28, num_k
                     head_dim: int = 128, min_prefix: int = 1024, max_prefix: int = 4096,
                     block: int = 32, active: int = 8, page_size: int = 32, step: int = 0,
                     dtype=torch.bfloat16, shuffle_pages: bool = True,
-                    layers: int = 1) -> PagedDecode:
+                    layers: int = 1, head_major: bool = False) -> PagedDecode:
     """Paged block-decode attention inputs. With layers > 1 the pools carry a leading
     layer dimension [layers, num_pages, page_size, Hkv, D] (one pool per layer, same
-    page table), the layout a 28-layer model step walks through."""
+    page table), the layout a 28-layer model step walks through. head_major=True stores
+    each page [Hkv, page_size, D] (one KV head's page is one contiguous run) and returns
+    the pools as [.., num_pages, page_size, Hkv, D] views of that storage; the values
+    are the same draws as the token-major pools."""
     g = _gen(seed)
     lo, hi = min_prefix // block, max_prefix // block
     prefix = block * torch.randint(lo, hi + 1, (batch,), generator=g)
@@ -113,6 +116,9 @@ def kv_decode_paged(seed: int = 0, batch: int = 16, num_q_heads: int = 28, num_k
     k = torch.randn(*shape, generator=g).to(dtype)
     v = torch.randn(*shape, generator=g).to(dtype)
     q = torch.randn(batch, active, num_q_heads, head_dim, generator=g).to(dtype)
+    if head_major:
+        k = k.transpose(-3, -2).contiguous().transpose(-3, -2)
+        v = v.transpose(-3, -2).contiguous().transpose(-3, -2)
     return PagedDecode(q, k, v, table, seqlens, prefix, page_size, step % max(1, block // active),
                        head_dim ** -0.5)
 

@@ -192,10 +192,11 @@ typedef struct fdllm_kv_attn_desc {
    * without q_start) before any key is read, positions outside [0, capacity) being
    * skipped (capacity = max_pages * page_size with a page table, else max_seqlen).
    * Replaces StaticKVCache.update (static_kv_cache.py:132-160) followed by the
-   * attention of the prefill / commit forward (modeling.py:385-411): the prefill
-   * kernels read these rows from k_new / v_new and store them from registers as they
-   * stage them, so the write costs no second read; other shapes launch the cache
-   * write kernel before the attention. */
+   * attention of the prefill / commit forward (modeling.py:385-411): without q_start
+   * the prefill kernels read these rows from k_new / v_new and store them from
+   * registers as they stage them, so the write costs no second read; other shapes,
+   * and every call with an explicit q_start (whose visible keys may run past the last
+   * new row), launch the cache write kernel before the attention. */
   const void* k_new;
   const void* v_new;
   int64_t new_stride_b, new_stride_s, new_stride_h;
@@ -213,6 +214,13 @@ typedef struct fdllm_kv_attn_desc {
  * the in-kernel write is the default (the 4 x 4096-token prefill: 473-475 us against
  * 479-480 us with the copy kernel, timed in rotation). */
 #define FDLLM_ATTN_CACHE_WRITE_KERNEL 4
+/* Sub-block decode shapes (at most 64 sequences, a page table of at most 4096 entries or
+ * none): deal the keys of all sequences evenly over the workgroups, in runs of 128-key
+ * quads that cross from one sequence into the next, instead of splitting each sequence's
+ * keys on its own. Results agree within rounding (the splits differ). Off by default: on
+ * the 16-sequence 7B step it measured slower (a workgroup whose run crosses a sequence
+ * boundary loses about one quad's time). */
+#define FDLLM_ATTN_BALANCED_SPLITS 8
 
 /* Bytes of device workspace fdllm_kv_attn_fwd needs for `desc` (0 when the call
  * is not split over several workgroups per KV head). The workspace starts with

@@ -1,7 +1,8 @@
-"""The C-ABI library: it loads on a machine without a GPU, exports every function
-that include/*.h declares, and the ctypes table binds exactly those functions.
-No kernel is launched here; argument checks that reject a call before any launch
-are exercised through the C ABI with null pointers.
+"""The C-ABI libraries: they load on a machine without a GPU and export every function
+their header declares (include/fdllm_hip.h: libfdllm_hip.so, whose ctypes table binds
+exactly those functions; include/fdllm_probes.h: libfdllm_probes.so, the measurement
+probes bench.py uses). No kernel is launched here; argument checks that reject a call
+before any launch are exercised through the C ABI with null pointers.
 """
 import ctypes
 import re
@@ -11,12 +12,18 @@ from pathlib import Path
 import pytest
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADERS = sorted((ROOT / "include").glob("*.h"))
+HEADERS = [ROOT / "include" / "fdllm_hip.h"]
+PROBES_HEADER = ROOT / "include" / "fdllm_probes.h"
+PROBES_LIB = ROOT / "fast_v2_amd" / "lib" / "libfdllm_probes.so"
 
 
-def _declared_functions():
+def test_every_header_is_checked():
+    assert sorted((ROOT / "include").glob("*.h")) == sorted(HEADERS + [PROBES_HEADER])
+
+
+def _declared_functions(headers=HEADERS):
     names = set()
-    for h in HEADERS:
+    for h in headers:
         text = h.read_text()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         text = re.sub(r"//[^\n]*", "", text)
@@ -49,6 +56,23 @@ def test_library_exports_every_declared_symbol(lib):
     assert not missing, f"declared but not exported: {sorted(missing)}"
     for name in _declared_functions():
         assert getattr(lib, name) is not None
+
+
+def test_probes_library_exports_its_header():
+    if not PROBES_LIB.exists():
+        pytest.fail(f"{PROBES_LIB} is not built (run __graft_entry__.build())")
+    names = _declared_functions([PROBES_HEADER])
+    assert names == {"fdllm_probe_read_kv", "fdllm_probe_copy_rows"}
+    out = subprocess.run(["nm", "-D", "--defined-only", str(PROBES_LIB)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
+    assert names <= exported
+    lib = ctypes.CDLL(str(PROBES_LIB))
+    # rejected arguments return before any launch (no GPU needed)
+    lib.fdllm_probe_copy_rows.restype = ctypes.c_int
+    assert lib.fdllm_probe_copy_rows(None, 16, 1, None, None, 1, 16, None) == -1
+    lib.fdllm_probe_read_kv.restype = ctypes.c_int
+    assert lib.fdllm_probe_read_kv(*([None] * 2 + [0] * 6 + [None, 0, 32, None, 1, 4, 64, None, None])) == -1
 
 
 def test_ctypes_table_matches_header():

@@ -257,12 +257,14 @@ def test_repeated_split_calls_rearm(gpu):
     assert torch.equal(first, again)
 
 
+@pytest.mark.parametrize("balanced", [False, True])
 @pytest.mark.parametrize("case", ["batch80_fixed_chunks", "one_long_capped", "batch64_all_lanes", "hkv1_256_slots"])
-def test_split_decode_partitions(gpu, case):
-    """The split decode kernel's key partition at its edges: more than 64 sequences (fixed
-    5120-key chunks), one sequence long enough to need the 16-split cap next to empty and
-    one-tile sequences, exactly 64 sequences (every lane of the search), and one KV head
-    (256 slots per head)."""
+def test_split_decode_partitions(gpu, case, balanced):
+    """The split decode kernels' key partitions at their edges: more than 64 sequences
+    (fixed 5120-key chunks), one sequence long enough to need the 16-split cap next to
+    empty and one-tile sequences, exactly 64 sequences (every lane of the search), and one
+    KV head (256 slots per head); balanced selects the runs across sequence boundaries
+    instead of the per-sequence splits."""
     g = torch.Generator().manual_seed(len(case))
     hq, hkv = 28, 4
     if case == "batch80_fixed_chunks":
@@ -281,15 +283,82 @@ def test_split_decode_partitions(gpu, case):
     k = torch.randn(B, max_s, hkv, D, generator=g).to(torch.bfloat16)
     v = torch.randn(B, max_s, hkv, D, generator=g).to(torch.bfloat16)
     sl = lens.to(torch.int32)
-    print(f"case partition {case} B={B} max_len={max_s}", flush=True)
+    print(f"case partition {case} balanced={balanced} B={B} max_len={max_s}", flush=True)
     if case == "batch80_fixed_chunks":
         # a split call with few sequences first fills the workspace right after the
         # counter region; the 320 counters of this call must not read those partials
         small = workloads.kv_decode_paged(seed=9, batch=4, min_prefix=2048, max_prefix=4096)
         ops.block_attn(small.q.to(gpu), small.k_pool.to(gpu), small.v_pool.to(gpu), small.seqlens.to(gpu),
                        small.scale, page_table=small.page_table.to(gpu), page_size=small.page_size)
-    out = ops.block_attn(q.to(gpu), k.to(gpu), v.to(gpu), sl.to(gpu))
+    out = ops.block_attn(q.to(gpu), k.to(gpu), v.to(gpu), sl.to(gpu), balanced_splits=balanced)
     _check(out, oa.attention_np(q.float(), k.float(), v.float(), sl))
+
+
+@pytest.mark.parametrize("case", ["many_short", "fewer_pairs_than_slots", "empty_runs", "all_empty",
+                                  "block_causal_qstart", "head_major_pages", "fp16_contig_bhsd", "gqa1_q64"])
+def test_balanced_decode_runs(gpu, case):
+    """The balanced split decode kernel (opt-in): runs of quads that cross sequence boundaries.
+    many_short: 64 sequences of 0-200 keys, so one workgroup's run spans many sequences
+    (more pieces than query blocks staged at the start); fewer_pairs_than_slots: 3
+    sequences of 1-2 pairs (only P of the slots work); empty_runs: empty sequences
+    between long ones; all_empty: every sequence empty (zero rows); block_causal_qstart:
+    the block-causal mask with explicit query starts; head_major_pages: a page pool stored
+    head-major; fp16_contig_bhsd: fp16 over a head-major contiguous cache; gqa1_q64: 64
+    query rows of one head per KV head. Each against the float64 oracle, and against the
+    default per-sequence splits (checked against the oracle too) within the same bound."""
+    g = torch.Generator().manual_seed(sum(map(ord, case)))
+    hq, hkv, Sq, D, dtype = 28, 4, 8, 128, torch.bfloat16
+    mode, qst, pt, page = _ffi.MASK_SEQLEN, None, None, 0
+    if case == "many_short":
+        lens = torch.randint(0, 201, (64,), generator=g)
+    elif case == "fewer_pairs_than_slots":
+        lens = torch.tensor([10, 64, 100])
+    elif case == "empty_runs":
+        lens = torch.tensor([3000, 0, 0, 2048, 0, 1, 4100, 0])
+    elif case == "all_empty":
+        lens = torch.zeros(5, dtype=torch.int64)
+    elif case == "block_causal_qstart":
+        lens = torch.randint(500, 3000, (12,), generator=g)
+        mode = _ffi.MASK_BLOCK_CAUSAL
+        qst = (lens - Sq - torch.randint(0, 40, (12,), generator=g)).clamp(min=0).to(torch.int32)
+    elif case == "head_major_pages":
+        lens = None
+    elif case == "fp16_contig_bhsd":
+        lens, dtype = torch.randint(1, 2500, (16,), generator=g), torch.float16
+    else:
+        hq, hkv, Sq = 4, 4, 64
+        lens = torch.randint(1, 1500, (10,), generator=g)
+    if case == "head_major_pages":
+        wl = workloads.kv_decode_paged(seed=3, batch=16, head_major=True)
+        q, k, v, sl, pt, page = wl.q, wl.k_pool, wl.v_pool, wl.seqlens, wl.page_table, wl.page_size
+        assert k.stride(1) == D and k.stride(2) == page * D  # one KV head's page is one contiguous run
+        exp = oa.attention_np(q.float(), k.float(), v.float(), sl, wl.scale, page_table=pt, page_size=page)
+    else:
+        B = len(lens)
+        max_s = max(1, int(lens.max()))
+        q = torch.randn(B, Sq, hq, D, generator=g).to(dtype)
+        k = torch.randn(B, max_s, hkv, D, generator=g).to(dtype)
+        v = torch.randn(B, max_s, hkv, D, generator=g).to(dtype)
+        if case == "fp16_contig_bhsd":
+            k = k.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+            v = v.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+        sl = lens.to(torch.int32)
+        exp = oa.attention_np(q.float(), k.float(), v.float(), sl, mask_mode=mode, mask_block=32, q_start=qst)
+    print(f"case balanced decode {case} B={q.shape[0]} lens={sl.tolist()}", flush=True)
+    args = dict(mask_mode=mode, mask_block=32, q_start=None if qst is None else qst.to(gpu),
+                page_table=None if pt is None else pt.to(gpu), page_size=page)
+    kd, vd = k.to(gpu), v.to(gpu)
+    assert kd.stride() == k.stride() and vd.stride() == v.stride()  # the copy keeps the storage order
+    out = ops.block_attn(q.to(gpu), kd, vd, sl.to(gpu), balanced_splits=True, **args)
+    _check(out, exp)
+    ref = ops.block_attn(q.to(gpu), kd, vd, sl.to(gpu), **args)
+    _check(out, ref.float().cpu().numpy())
+    _check(ref, exp)
+    if case == "all_empty":
+        assert torch.count_nonzero(out) == 0 and torch.count_nonzero(ref) == 0
+    # a second call re-arms the arrival counters: identical output
+    again = ops.block_attn(q.to(gpu), kd, vd, sl.to(gpu), balanced_splits=True, **args)
+    assert torch.equal(out, again)
 
 
 @pytest.mark.parametrize("batch,page_size", [(16, 32), (40, 16)])
@@ -622,8 +691,10 @@ def test_block_decode_split_prefill_kernel(gpu, case):
     "prefix_paged64_fp16",      # fp16, 64-key pages, prefix on a page boundary
     "commit_split_paged32",     # a whole 32-token block per sequence: split prefill kernel
     "commit_split_misaligned",  # the same with prefixes that are not multiples of 32
-    "short_visible_qstart",     # new rows past the visible length: copied after the loop
+    "short_visible_qstart",     # explicit q_start, new rows past the visible length
     "past_capacity",            # new rows past the cache's end are dropped
+    "qstart_cache_past_new",    # explicit q_start, visible cache rows past the last new row
+    "qstart_block_causal",      # explicit unaligned q_start, block-causal, cache rows past the new ones
     "subblock_fallback",        # 8 queries: split decode kernel, cache write kernel first
     "head64_fallback",          # head_dim 64: the general kernel, cache write kernel first
 ])
@@ -631,8 +702,8 @@ def test_block_decode_split_prefill_kernel(gpu, case):
 def test_fused_cache_write(gpu, case, in_kernel):
     """k_new / v_new: the call stores the query tokens' K / V rows into the cache at
     q_start + t and attends over the updated cache, from inside the prefill kernels
-    (in_kernel, where the shape has them) or by its copy kernel
-    (FDLLM_ATTN_CACHE_WRITE_KERNEL). The cache must equal
+    (in_kernel, where the shape has them and q_start is implicit) or by its copy kernel
+    (FDLLM_ATTN_CACHE_WRITE_KERNEL, and every call with an explicit q_start). The cache must equal
     the oracle's write bit for bit, the output must equal the same call made as a
     separate cache write followed by the attention (bit for bit) and match the float64
     oracle over the written cache."""
@@ -652,6 +723,12 @@ def test_fused_cache_write(gpu, case, in_kernel):
         B, Sq, qs, cap, lens, mode, explicit_qs = 2, 400, [96, 10], 600, [446, 330], _ffi.MASK_SEQLEN, True
     elif case == "past_capacity":
         B, Sq, qs, cap, lens, explicit_qs = 1, 600, [100], 650, [650], True
+    elif case == "qstart_cache_past_new":
+        # keys [q_start + Sq, seqlens) are cache rows this call does not write: they
+        # must be read from the cache, not from the new rows of the next sequence
+        B, Sq, qs, cap, lens, mode, explicit_qs = 3, 300, [40, 0, 257], 900, [440, 400, 657], _ffi.MASK_SEQLEN, True
+    elif case == "qstart_block_causal":
+        B, Sq, qs, cap, lens, page, explicit_qs = 2, 270, [45, 301], 960, [415, 700], 32, True
     elif case == "subblock_fallback":
         B, Sq, qs, cap, lens, page = 4, 8, [1000, 500, 64, 2047], 2112, None, 32
     else:
