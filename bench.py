@@ -16,7 +16,8 @@ stream give the per-step time, i.e. the average kernel duration plus the
 inter-kernel gap.
 
 Also reported (same run, under "extra"): the same step with all 32 block queries
-active (the full-block forward), gather + RMSNorm (bf16 [4096 x 3584], 1024 rows) and
+active (the full-block forward), gather + RMSNorm (bf16 [4096 x 3584], 1024 rows), the
+row scatter of those 1024 rows back into two [4096 x 3584] destinations, and
 block-causal prefill with its KV-cache write (4 x 4096 tokens), each with its own
 roofline.
 
@@ -283,6 +284,8 @@ def bench_decode_full(torch, args):
     layers = args.layers
     gen = torch.Generator(device=dev).manual_seed(1)
     kp = torch.empty((layers,) + tuple(wl.k_pool.shape), dtype=wl.k_pool.dtype, device=dev)
+    if args.layout == "paged_hm":  # the headline's page layout: [Hkv, page_size, D] per page
+        kp = kp.transpose(-3, -2).contiguous().transpose(-3, -2)
     vp = torch.empty_like(kp)
     kp.normal_(generator=gen)
     vp.normal_(generator=gen)
@@ -394,6 +397,49 @@ def bench_gather(torch, args):
                  "node, each as a graph of the same length as the gather's"),
     }
     del hs, dst
+    torch.cuda.empty_cache()
+    return res
+
+
+def bench_scatter(torch, args):
+    """The row scatter at the gather's size (scatter_and_return_cuda,
+    fused_gather_norm.cu:79-119): 1024 rows of 3584 bf16 written back to two
+    [1, 4096, 3584] destinations (the block cache and the current hidden states). The
+    values and destination pairs rotate through 24 sets (24 x 66 MB), so every call reads
+    and writes HBM rather than the last-level cache."""
+    from fast_v2_amd import ops, workloads
+
+    dev = torch.device("cuda", 0)
+    wl = workloads.gather_rmsnorm_rows(seed=0)
+    B, S, H = wl.hidden.shape
+    T = wl.indices.shape[1]
+    sets = 24
+    g = torch.Generator().manual_seed(1)
+    vals0 = torch.randn(B, T, H, generator=g).to(wl.hidden.dtype)
+    vals = [vals0.to(dev)] + [torch.empty_like(vals0, device=dev) for _ in range(sets - 1)]
+    for v in vals[1:]:
+        v.copy_(vals[0])
+    caches = [wl.hidden.to(dev) for _ in range(sets)]
+    curs = [c.clone() for c in caches]
+    idx = wl.indices.to(dev)
+
+    def step(i):
+        j = i % sets
+        ops.scatter_rows(vals[j], idx, caches[j], curs[j])
+
+    # bit-exact against torch's scatter_ on the first set
+    step(0)
+    torch.cuda.synchronize()
+    exp = wl.hidden.clone().scatter_(1, wl.indices.unsqueeze(-1).expand(-1, -1, H), vals0).to(dev)
+    if not (torch.equal(caches[0], exp) and torch.equal(curs[0], exp)):
+        raise RuntimeError("scatter: the destinations differ from torch's scatter_")
+    us = _time_graph(torch, step, args.gather_steps, min(args.warmup, 32))
+    nbytes = workloads.scatter_bytes(T, H, 2, destinations=2)
+    gbs = nbytes / (us * 1e-6) / 1e9
+    res = {"us_per_call": us, "bytes_per_call": nbytes, "achieved_gbs": gbs,
+           "roofline": _roofline("hbm", gbs, HBM_PEAK_GBS, "GB/s", _traffic("scatter_rows")),
+           "shape": {"rows": T, "hidden": H, "seq_len": S, "destinations": 2, "dtype": "bf16"}}
+    del vals, caches, curs, exp
     torch.cuda.empty_cache()
     return res
 
@@ -643,6 +689,27 @@ def cpu_baseline_gather(torch):
                        "oracle/gather_rmsnorm.py), the whole call (gathered + normed outputs)")
 
 
+def cpu_baseline_scatter(torch):
+    """Reference CPU path for the row scatter: torch's scatter_ (the reference's PyTorch
+    statement of this step, cuda_bench/bench_sparse_cuda.py:88-96) into both destinations
+    of scatter_and_return_cuda, bf16 [1, 4096, 3584], 1024 rows; the whole call."""
+    from fast_v2_amd import workloads
+
+    wl = workloads.gather_rmsnorm_rows(seed=0)
+    H = wl.hidden.shape[2]
+    vals = torch.randn(1, wl.indices.shape[1], H, generator=torch.Generator().manual_seed(1)).to(wl.hidden.dtype)
+    cache, cur = wl.hidden.clone(), wl.hidden.clone()
+    ii = wl.indices.unsqueeze(-1).expand(-1, -1, H)
+
+    def call():
+        cache.scatter_(1, ii, vals)
+        cur.scatter_(1, ii, vals)
+    st = _cpu_protocol(torch, call)
+    return _cpu_result(st, "us/call", "torch CPU scatter_ of the 1024 bf16 rows into both [1, 4096, 3584] "
+                       "destinations (cuda_bench/bench_sparse_cuda.py:88-96, applied to the cache and the "
+                       "current hidden states as scatter_and_return_cuda writes them), the whole call")
+
+
 def cpu_baseline_prefill(torch):
     """Reference CPU path for block-causal prefill: SDPA with the block-causal bool mask
     (modeling.py:145-150, :398-411) on sequence 0 of the 4; value = 4 x that time."""
@@ -745,7 +812,8 @@ def main() -> int:
     ap.add_argument("--balanced-splits", action="store_true",
                     help="decode: deal all sequences' keys evenly over the workgroups (runs across sequences)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", choices=["decode", "decode_full", "gather", "prefill", "e2e", "qkv"], default=None)
+    ap.add_argument("--only", choices=["decode", "decode_full", "gather", "scatter", "prefill", "e2e", "qkv"],
+                    default=None)
     ap.add_argument("--e2e-tokens", type=int, default=1024, help="tokens generated in the end-to-end leg")
     ap.add_argument("--no-e2e", action="store_true", help="skip the end-to-end generation leg")
     ap.add_argument("--e2e-weights", default=None,
@@ -798,6 +866,10 @@ def main() -> int:
         _log(f"gather: normed {g['normed']['us_per_call']:.3f} us, pair {g['pair']['us_per_call']:.3f} us; "
              f"plain copy of the rows {g['ceiling']['copy_us_per_call']:.3f} us, empty kernel node "
              f"{g['ceiling']['empty_kernel_us_per_node']:.3f} us")
+    if args.only in (None, "scatter"):
+        extra["scatter_rows"] = bench_scatter(torch, args)
+        _log(f"scatter: {extra['scatter_rows']['us_per_call']:.3f} us, "
+             f"{extra['scatter_rows']['achieved_gbs']:.0f} GB/s")
     if args.only is None:
         extra["small_fp32"] = bench_small_fp32(torch, args)
         _log(f"small fp32 (config 1): {extra['small_fp32']['us_per_call']:.2f} us per call")
@@ -825,6 +897,9 @@ def main() -> int:
         if "gather_rmsnorm" in extra:
             _log("cpu baseline (gather + RMSNorm) ...")
             extra["gather_rmsnorm"]["cpu_baseline"] = cpu_baseline_gather(torch)
+        if "scatter_rows" in extra:
+            _log("cpu baseline (row scatter) ...")
+            extra["scatter_rows"]["cpu_baseline"] = cpu_baseline_scatter(torch)
         if "prefill" in extra:
             _log("cpu baseline (prefill sample) ...")
             extra["prefill"]["cpu_baseline"] = cpu_baseline_prefill(torch)

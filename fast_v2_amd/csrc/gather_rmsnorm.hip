@@ -200,14 +200,15 @@ __global__ __launch_bounds__(64 * kGatherRows) void gather_rmsnorm_vec_kernel(co
 
   const u32x4* hrow = reinterpret_cast<const u32x4*>(hbase + src * hs_s);
   // All loads are issued unconditionally and back to back, so the whole row is in flight
-  // at once. nvec lies in (64 (VPL - 1), 64 VPL], so only the last vector can run past the
+  // at once; they are non-temporal (each row is read once: 4.42 -> 4.08 us per call at
+  // 1024 rows x 3584 bf16, against 3.79 us for a plain gathered copy of the rows). nvec lies in (64 (VPL - 1), 64 VPL], so only the last vector can run past the
   // row end: its index is clamped and its lanes past the end are zeroed afterwards.
   const int clast = lane + kWave * (VPL - 1);
   const bool last_in = clast < nvec;
   u32x4 x[VPL];
 #pragma unroll
-  for (int v = 0; v < VPL - 1; ++v) x[v] = hrow[lane + kWave * v];
-  x[VPL - 1] = hrow[last_in ? clast : nvec - 1];
+  for (int v = 0; v < VPL - 1; ++v) x[v] = __builtin_nontemporal_load(hrow + lane + kWave * v);
+  x[VPL - 1] = __builtin_nontemporal_load(hrow + (last_in ? clast : nvec - 1));
   float w[VPL][N];
 #pragma unroll
   for (int v = 0; v < VPL - 1; ++v) load_weight<T, WK, N>(a.weight, (lane + kWave * v) * N, w[v]);
@@ -338,6 +339,43 @@ __global__ __launch_bounds__(256) void scatter_rows_kernel(const ScatterArgs a) 
       const uint16_t v = reinterpret_cast<const uint16_t*>(src)[i];
       reinterpret_cast<uint16_t*>(c)[i] = v;
       if (u) reinterpret_cast<uint16_t*>(u)[i] = v;
+    }
+  }
+}
+
+// The 16-byte-aligned form: one wave per source row, the row's VPL vectors per lane all
+// loaded before any store (the element loop above waits for each load in turn, since the
+// destinations may alias the values as far as the compiler knows). grid (B * T). Loads and
+// stores are non-temporal (streaming): at 1024 rows x 3584 bf16 into two destinations
+// this took the call from 6.90 to 4.77 us (plain loads with streaming stores: 5.0 us).
+template <int VPL>
+__global__ __launch_bounds__(64) void scatter_rows_vec_kernel(const ScatterArgs a) {
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int b = static_cast<int>(row / a.T);
+  const int t = static_cast<int>(row - static_cast<int64_t>(b) * a.T);
+  const int64_t dst = a.idx[b * a.is_b + t];
+  if (dst < 0 || dst >= a.S) return;  // uniform: one row per wave
+  const int nvec = a.H * a.esize / 16;
+  const u32x4* src = reinterpret_cast<const u32x4*>(static_cast<const char*>(a.values) + row * a.H * a.esize);
+  u32x4* c = reinterpret_cast<u32x4*>(static_cast<char*>(a.cache) + (b * a.cs_b + dst * a.cs_s) * a.esize);
+  u32x4 x[VPL];
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int i = lane + kWave * v;
+    x[v] = i < nvec ? __builtin_nontemporal_load(src + i) : u32x4{0u, 0u, 0u, 0u};
+  }
+#pragma unroll
+  for (int v = 0; v < VPL; ++v) {
+    const int i = lane + kWave * v;
+    if (i < nvec) __builtin_nontemporal_store(x[v], c + i);
+  }
+  if (a.cur) {
+    u32x4* u = reinterpret_cast<u32x4*>(static_cast<char*>(a.cur) + (b * a.us_b + dst * a.us_s) * a.esize);
+#pragma unroll
+    for (int v = 0; v < VPL; ++v) {
+      const int i = lane + kWave * v;
+      if (i < nvec) __builtin_nontemporal_store(x[v], u + i);
     }
   }
 }
@@ -642,8 +680,18 @@ extern "C" int fdllm_scatter_rows(const void* values, const int64_t* indices, in
             (current == nullptr || aligned16(current)) && (cache_batch_stride * es) % 16 == 0 && (cache_row_stride * es) % 16 == 0 &&
             (current_batch_stride * es) % 16 == 0 && (current_row_stride * es) % 16 == 0;
   const int64_t rows = static_cast<int64_t>(batch) * num_tokens;
-  scatter_rows_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0,
-                        static_cast<hipStream_t>(stream)>>>(a);
+  FDLLM_CHECK_ARG(rows <= INT32_MAX, "fdllm_scatter_rows: %lld rows exceed the grid", static_cast<long long>(rows));
+  const hipStream_t s = static_cast<hipStream_t>(stream);
+  const int64_t nvec = a.vec16 ? static_cast<int64_t>(hidden_size) * es / 16 : 0;
+  if (a.vec16 && nvec <= kWave * 8) {
+    const dim3 grid(static_cast<unsigned>(rows));
+    if (nvec <= kWave * 2) scatter_rows_vec_kernel<2><<<grid, dim3(kWave), 0, s>>>(a);
+    else if (nvec <= kWave * 4) scatter_rows_vec_kernel<4><<<grid, dim3(kWave), 0, s>>>(a);
+    else if (nvec <= kWave * 6) scatter_rows_vec_kernel<6><<<grid, dim3(kWave), 0, s>>>(a);
+    else scatter_rows_vec_kernel<8><<<grid, dim3(kWave), 0, s>>>(a);
+  } else {
+    scatter_rows_kernel<<<dim3(static_cast<unsigned>((rows + 3) / 4)), dim3(256), 0, s>>>(a);
+  }
   FDLLM_RETURN_LAUNCH_STATUS("fdllm_scatter_rows");
 }
 

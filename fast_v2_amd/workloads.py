@@ -72,6 +72,12 @@ def gather_bytes(rows: int, hidden: int, elem: int = 2, with_gathered: bool = Fa
     return rows * per_row * (3 if with_gathered else 2) + hidden * elem + rows * index_bytes
 
 
+def scatter_bytes(rows: int, hidden: int, elem: int = 2, destinations: int = 2, index_bytes: int = 8) -> int:
+    """Algorithmic HBM bytes of one row scatter: read each value row once, write it to every
+    destination, read the indices."""
+    return rows * hidden * elem * (1 + destinations) + rows * index_bytes
+
+
 # ---------------------------------------------------------------------------
 @dataclass
 class PagedDecode:

@@ -13,6 +13,8 @@ ref_gather_pair_plain      fused_gather_input_rmsnorm_pair host fn (fused_gather
                            returns (g, g*inv) without a weight.
 gather_rmsnorm_np          the same three modes in float64 numpy, with explicit
                            round-to-nearest-even to bf16/fp16 where the reference rounds.
+scatter_rows_np            scatter_and_return_cuda (fused_gather_norm.cu:79-119): the
+                           rows written back to two [B, S, H] destinations.
 """
 from __future__ import annotations
 
@@ -101,3 +103,26 @@ def gather_rmsnorm_np(hidden: np.ndarray, indices: np.ndarray, weight, eps: floa
     else:
         raise ValueError(mode)
     return round_to(g, dtype), normed
+
+
+def scatter_rows_np(values: np.ndarray, indices: np.ndarray, cache: np.ndarray,
+                    current: np.ndarray | None = None):
+    """scatter_and_return_kernel / scatter_and_return_cuda (cuda_bench/fused_gather_norm.cu:79-119):
+    cache[b, indices[b, t]] = values[b, t] and the same into current, which is returned.
+    The reference's PyTorch statement of the same step is the scatter_ of
+    cuda_bench/bench_sparse_cuda.py:88-96 (pytorch_roundtrip). Indices outside [0, S) leave both destinations
+    untouched (the reference kernel does not check them). Works on copies; returns
+    (cache, current)."""
+    v = np.asarray(values)
+    idx = np.asarray(indices).astype(np.int64)
+    c = np.array(cache, copy=True)
+    u = None if current is None else np.array(current, copy=True)
+    S = c.shape[1]
+    for b in range(v.shape[0]):
+        for t in range(v.shape[1]):
+            r = idx[b, t]
+            if 0 <= r < S:
+                c[b, r] = v[b, t]
+                if u is not None:
+                    u[b, r] = v[b, t]
+    return c, u

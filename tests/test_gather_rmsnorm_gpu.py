@@ -114,7 +114,7 @@ def test_reference_fp32_entry_points(gpu):
     torch.testing.assert_close(n_got.cpu(), n_ref, atol=1e-5, rtol=1e-5)
 
 
-@pytest.mark.parametrize("H", [3584, 4096, 100, 1000, 8200])
+@pytest.mark.parametrize("H", [3584, 4096, 100, 1000, 8200, 2056, 8192, 2048])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_hidden_sizes_and_fp16(gpu, H, dtype):
     print(f"case H={H} {dtype}", flush=True)
@@ -132,7 +132,7 @@ def test_hidden_sizes_and_fp16(gpu, H, dtype):
 
 
 @pytest.mark.parametrize("H,dtype,tag", [
-    (2056, torch.bfloat16, "bf16"),   # 257 16-byte vectors: 5 per lane, the last one ragged
+    (2056, torch.bfloat16, "bf16"),   # 257 16-byte vectors: the last one held by a single lane
     (6152, torch.bfloat16, "bf16"),   # 769 vectors: 13 per lane, the generic path
     (8192, torch.float16, "f16"),     # 1024 vectors: the widest row held in registers
     (3588, torch.float32, "f32"),     # fp32 rows, 897 vectors: the generic path
@@ -207,21 +207,51 @@ def test_empty_and_errors(gpu):
         ops.gather_rmsnorm(hidden.cpu(), idx.cpu(), None, 1e-6, og.NORM_PLAIN, True)
 
 
-def test_scatter_rows(gpu):
-    g = torch.Generator().manual_seed(5)
-    B, S, T, H = 2, 40, 7, 384
-    vals = torch.randn(B, T, H, generator=g).to(torch.bfloat16)
+def _np_bits(t: torch.Tensor) -> np.ndarray:
+    """The tensor's bit patterns as integers (bit-exact comparison of any 2- or 4-byte dtype)."""
+    t = t.detach().cpu().contiguous()
+    return t.view(torch.int16 if t.element_size() == 2 else torch.int32).numpy()
+
+
+@pytest.mark.parametrize("B,S,T,H,dtype,two,row_pad,bad", [
+    (2, 40, 7, 384, torch.bfloat16, True, 0, False),       # 48 vectors per row
+    (1, 4096, 1024, 3584, torch.bfloat16, True, 0, False),  # the 1024 x 3584 workload, two destinations
+    (2, 64, 9, 4096, torch.float16, True, 0, False),       # 512 vectors: the largest register-staged row
+    (1, 64, 5, 8192, torch.bfloat16, True, 0, False),      # 1024 vectors: the looped row path
+    (2, 30, 6, 37, torch.bfloat16, True, 0, False),        # 74-byte rows: element loop
+    (2, 30, 6, 100, torch.float32, True, 0, False),        # fp32, 25 vectors
+    (3, 50, 11, 256, torch.bfloat16, False, 0, False),     # one destination
+    (2, 48, 8, 512, torch.bfloat16, True, 64, True),       # padded rows, out-of-range indices skipped
+])
+def test_scatter_rows(gpu, B, S, T, H, dtype, two, row_pad, bad):
+    """fdllm_scatter_rows bit-exact against the oracle (scatter_and_return_cuda,
+    fused_gather_norm.cu:79-119) and torch's scatter_; rows no index names keep their
+    contents."""
+    g = torch.Generator().manual_seed(5 + H)
+    vals = torch.randn(B, T, H, generator=g).to(dtype)
     idx = torch.stack([torch.randperm(S, generator=g)[:T] for _ in range(B)])
-    cache = torch.randn(B, S, H, generator=g).to(torch.bfloat16)
-    cur = torch.randn(B, S, H, generator=g).to(torch.bfloat16)
-    exp_cache, exp_cur = cache.clone(), cur.clone()
-    ii = idx.unsqueeze(-1).expand(-1, -1, H)
-    exp_cache.scatter_(1, ii, vals)
-    exp_cur.scatter_(1, ii, vals)
-    c_gpu, u_gpu = cache.to(gpu), cur.to(gpu)
-    ret = ops.scatter_rows(vals.to(gpu), idx.to(gpu), c_gpu, u_gpu)
-    assert ret.data_ptr() == u_gpu.data_ptr()
-    assert torch.equal(c_gpu.cpu(), exp_cache) and torch.equal(u_gpu.cpu(), exp_cur)
+    if bad:
+        idx[0, 1], idx[1, 3] = -1, S
+    base_c = torch.randn(B, S, H + row_pad, generator=g).to(dtype)
+    base_u = torch.randn(B, S, H + row_pad, generator=g).to(dtype)
+    exp_c, exp_u = og.scatter_rows_np(_np_bits(vals), idx.numpy(), _np_bits(base_c[..., :H]),
+                                      _np_bits(base_u[..., :H]) if two else None)
+    if not bad:
+        ii = idx.unsqueeze(-1).expand(-1, -1, H)
+        assert np.array_equal(_np_bits(base_c[..., :H].clone().scatter_(1, ii, vals)), exp_c)
+    c_full, u_full = base_c.to(gpu), base_u.to(gpu)
+    c_gpu, u_gpu = c_full[..., :H], u_full[..., :H]
+    ret = ops.scatter_rows(vals.to(gpu), idx.to(gpu), c_gpu, u_gpu if two else None)
+    torch.cuda.synchronize()
+    assert np.array_equal(_np_bits(c_gpu), exp_c)
+    if two:
+        assert ret.data_ptr() == u_gpu.data_ptr()
+        assert np.array_equal(_np_bits(u_gpu), exp_u)
+    else:
+        assert ret is None
+        assert torch.equal(u_full.cpu(), base_u)
+    if row_pad:  # the padding columns are never written
+        assert torch.equal(c_full[..., H:].cpu(), base_c[..., H:])
 
 
 @pytest.mark.parametrize("rows,H,dtype", [

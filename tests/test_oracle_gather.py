@@ -122,3 +122,34 @@ def test_bf16_rounding_matches_torch():
     x = torch.cat([x, ties])
     exp = x.to(torch.bfloat16).float().numpy()
     np.testing.assert_array_equal(og.round_f32_to_bf16(x.numpy()), exp)
+
+
+def test_scatter_oracle_against_torch_scatter_and_round_trip():
+    """scatter_rows_np (fused_gather_norm.cu:79-119) against torch's scatter_ into both
+    destinations; gathering the scattered rows back gives the values; rows no index names
+    keep their old contents; an out-of-range index changes nothing; a planted off-by-one
+    row index fails."""
+    g = torch.Generator().manual_seed(3)
+    B, S, T, H = 3, 50, 11, 24
+    vals = torch.randn(B, T, H, generator=g)
+    idx = torch.stack([torch.randperm(S, generator=g)[:T] for _ in range(B)])
+    cache = torch.randn(B, S, H, generator=g)
+    cur = torch.randn(B, S, H, generator=g)
+    c, u = og.scatter_rows_np(vals.numpy(), idx.numpy(), cache.numpy(), cur.numpy())
+    ii = idx.unsqueeze(-1).expand(-1, -1, H)
+    np.testing.assert_array_equal(c, cache.clone().scatter_(1, ii, vals).numpy())
+    np.testing.assert_array_equal(u, cur.clone().scatter_(1, ii, vals).numpy())
+    for b in range(B):
+        np.testing.assert_array_equal(c[b, idx[b].numpy()], vals[b].numpy())
+        untouched = np.setdiff1d(np.arange(S), idx[b].numpy())
+        np.testing.assert_array_equal(c[b, untouched], cache[b, untouched].numpy())
+        np.testing.assert_array_equal(u[b, untouched], cur[b, untouched].numpy())
+    bad = idx.clone()
+    bad[1, 4] = S
+    bad[2, 0] = -1
+    c2, u2 = og.scatter_rows_np(vals.numpy(), bad.numpy(), cache.numpy(), None)
+    assert u2 is None
+    np.testing.assert_array_equal(c2[1, idx[1, 4]], cache[1, idx[1, 4]].numpy())
+    np.testing.assert_array_equal(c2[2, idx[2, 0]], cache[2, idx[2, 0]].numpy())
+    planted, _ = og.scatter_rows_np(vals.numpy(), ((idx + 1) % S).numpy(), cache.numpy())
+    assert not np.array_equal(planted, c)
