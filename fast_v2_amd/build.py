@@ -31,7 +31,7 @@ HEADER = REPO_DIR / "include" / "fdllm_hip.h"
 PROBES_HEADER = REPO_DIR / "include" / "fdllm_probes.h"
 
 SOURCES = [CSRC / "gather_rmsnorm.hip", CSRC / "block_attn.hip", CSRC / "rope_kv.hip", CSRC / "sampler.hip"]
-DEPS = SOURCES + [CSRC / "fdllm_common.h", HEADER]
+DEPS = SOURCES + [CSRC / "fdllm_common.h", CSRC / "attn_plan.h", CSRC / "host_errors.h", HEADER]
 PROBES_SOURCES = [CSRC / "probes.hip"]
 PROBES_DEPS = PROBES_SOURCES + [PROBES_HEADER]
 

@@ -39,19 +39,17 @@
 #include <mutex>
 
 #include "fdllm_common.h"
+#include "attn_plan.h"
 
 namespace fdllm {
 namespace {
 
-constexpr int kKT = 64;        // keys per tile
-constexpr int kThreads = 256;  // 4 waves
 constexpr int kSlcNt = 2;      // buffer-load cache policy: streaming (no reuse expected)
 // Buffer load/store cache policy "sc1": coherent at device scope. With 8 XCDs the L2
 // caches are per XCD; sc1 stores write through to memory and sc1 loads do not hit
 // another XCD's stale copy, which is all a cross-workgroup handoff of a few KiB needs
 // (the agent-scope fences of the HIP memory model write back and invalidate whole L2s).
 constexpr int kSc1 = 16;
-constexpr int kMaxDecodeSplits = 16;  // key splits per (sequence, KV head) in the split decode kernel
 #ifndef FDLLM_DECODE_STAGES
 #define FDLLM_DECODE_STAGES 2
 #endif
@@ -69,11 +67,10 @@ constexpr int kDecodeStages = FDLLM_DECODE_STAGES;  // tiles in flight per workg
 #ifndef FDLLM_XCD_SLOTS
 #define FDLLM_XCD_SLOTS 1
 #endif
-// Waves (x 32 query rows) per prefill workgroup. Measured and not kept: 4 waves (two
-// independent workgroups per CU, so that their softmax and MFMA phases drift apart):
-// 549 us against 516-523 us for the 4 x 4096 prefill, the doubled K/V staging per
-// thread pushed it to 256 VGPRs with spills.
-constexpr int kPrefillWaves = 8;
+// Prefill workgroups have kPrefillWaves = 8 waves (x 32 query rows). Measured and not
+// kept: 4 waves (two independent workgroups per CU, so that their softmax and MFMA phases
+// drift apart): 549 us against 516-523 us for the 4 x 4096 prefill, the doubled K/V
+// staging per thread pushed it to 256 VGPRs with spills.
 
 struct AttnParams {
   const uint16_t* q;
@@ -821,8 +818,6 @@ __device__ __forceinline__ int ceil_div_small(int a, int b) {
   return q;
 }
 
-constexpr int kDecodeMaxTiles = 160;  // 32-key tiles per split: page ids staged in LDS
-
 // Key range of one workgroup of the split decode kernel.
 struct DecodePart {
   int b;       // sequence, -1 for an idle workgroup
@@ -1392,7 +1387,6 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
 // whole page table in LDS (batch * max_pages <= kBalMaxPages) or a contiguous cache,
 // head_dim 128, at most 64 query rows per KV head.
 constexpr int kBalQSlots = 3;
-constexpr int kBalMaxPages = 4096;
 // LDS placement of the balanced decode kernel's regions (byte offsets in one arena): team
 // 0's two tile buffers, team 1's, the query blocks, the page table, the per-sequence
 // facts. (Five placements of the team buffers relative to the query blocks and the 80 KB
@@ -1878,9 +1872,8 @@ __device__ __forceinline__ float halves_sum(float v) {
 // query rows per wave of kv_attn_f32_kernel: on the 12 / 2-head block of 32 queries over
 // 544 keys, 1: 27.8 us, 2: 36.2 us, 4: 72.9 us (fewer rows per workgroup, more workgroups
 // in flight; the previous one-wave-per-row form without staging: 85 us)
-#ifndef FDLLM_F32_ROWS_PER_WAVE
-#define FDLLM_F32_ROWS_PER_WAVE 1
-#endif
+// (FDLLM_F32_ROWS_PER_WAVE, the rows per wave, is set in attn_plan.h: the plan sizes the
+// grid from it.)
 template <int DPL, bool PAGED>
 __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
   constexpr int D = 64 * DPL;
@@ -3334,281 +3327,13 @@ __global__ __launch_bounds__(256) void kv_write_kernel(const KVWriteArgs a) {
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+// The plan (kernel family, workspace, grids, argument checks) is host-only code in
+// attn_plan.h; the launchers below take the grids it computes.
 
-// Kernel families a call can take (make_plan picks one per descriptor).
-enum PlanKind {
-  kPlanGeneral = 0,
-  kPlanAllHeads = 1,
-  kPlanSplitDecode = 2,
-  kPlanPrefill = 3,
-  kPlanSplitPrefill = 4,
-  kPlanF32 = 5,
-  kPlanBalancedDecode = 6
-};
-
-struct Plan {
-  int kind;     // PlanKind
-  bool decode;  // all-heads decode kernel (kv_decode_kernel)
-  int MT, rows_per_wg, n_rb, n_splits, chunk, R;
-  size_t ws_o_bytes, ws_ml_bytes;
-  size_t ws_unit_off;  // split prefill: byte offset of the unit table in the (m, l) region
-};
-
-// Split-KV decode plan. By default the kernel partitions the keys itself from the
-// device-side lengths (balanced mode) over S slots per KV head, S * Hkv ~ one
-// workgroup per CU; a caller-given kv_split fixes the keys per split instead.
-constexpr int kSplitTargetWG = 256;                   // MI355X compute units
-constexpr int kSplitMaxChunk = kDecodeMaxTiles * 32;  // keys per split: page ids staged in LDS
-constexpr int kBalancedMaxBatch = 64;                 // one wave lane per sequence in the partition search
-constexpr size_t kCounterBytes = 64 * 1024;           // arrival counters at the head of the workspace
-
-int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
-  FDLLM_CHECK_ARG(d != nullptr, "fdllm_kv_attn: null descriptor");
-  pl->ws_unit_off = 0;
-  FDLLM_CHECK_ARG(d->dtype == FDLLM_DTYPE_BF16 || d->dtype == FDLLM_DTYPE_F16 || d->dtype == FDLLM_DTYPE_F32,
-                  "fdllm_kv_attn: dtype %d unsupported (bf16, fp16 or fp32)", d->dtype);
-  FDLLM_CHECK_ARG(d->head_dim == 64 || d->head_dim == 128, "fdllm_kv_attn: head_dim %d unsupported (64 or 128)",
-                  d->head_dim);
-  FDLLM_CHECK_ARG(d->batch >= 0 && d->q_len >= 0 && d->num_q_heads > 0 && d->num_kv_heads > 0,
-                  "fdllm_kv_attn: bad sizes");
-  FDLLM_CHECK_ARG(d->num_q_heads % d->num_kv_heads == 0, "fdllm_kv_attn: num_q_heads %d not a multiple of %d",
-                  d->num_q_heads, d->num_kv_heads);
-  FDLLM_CHECK_ARG(d->max_seqlen >= 0, "fdllm_kv_attn: max_seqlen < 0");
-  FDLLM_CHECK_ARG(d->mask_mode >= FDLLM_MASK_SEQLEN && d->mask_mode <= FDLLM_MASK_BLOCK_CAUSAL,
-                  "fdllm_kv_attn: unknown mask_mode %d", d->mask_mode);
-  FDLLM_CHECK_ARG(d->mask_mode != FDLLM_MASK_BLOCK_CAUSAL || d->mask_block > 0,
-                  "fdllm_kv_attn: block-causal mask needs mask_block > 0");
-  if (d->dtype == FDLLM_DTYPE_F32) {
-    // fp32: kv_attn_f32_kernel, no workspace, no key split; pages of any power of two
-    FDLLM_CHECK_ARG(d->page_table == nullptr ||
-                        (d->page_size > 0 && (d->page_size & (d->page_size - 1)) == 0 && d->max_pages > 0),
-                    "fdllm_kv_attn: page table needs a power-of-two page_size and max_pages > 0");
-    FDLLM_CHECK_ARG(d->k_new == nullptr && d->v_new == nullptr,
-                    "fdllm_kv_attn: the cache write (k_new / v_new) takes bf16 or fp16 only");
-    const int64_t rows = static_cast<int64_t>(d->q_len) * d->num_q_heads;
-    FDLLM_CHECK_ARG(rows < (int64_t{1} << 31) - 4, "fdllm_kv_attn: q_len * num_q_heads too large");
-    pl->kind = kPlanF32;
-    pl->decode = false;
-    pl->MT = 0;
-    pl->rows_per_wg = 4 * FDLLM_F32_ROWS_PER_WAVE;
-    pl->n_rb = 1;
-    pl->n_splits = 1;
-    pl->chunk = 0;
-    pl->R = static_cast<int>(std::min<int64_t>(rows, 1 << 30));
-    pl->ws_o_bytes = pl->ws_ml_bytes = 0;
-    return FDLLM_OK;
-  }
-  // Each thread stages aligned groups of 2048 / head_dim keys from one page.
-  FDLLM_CHECK_ARG(d->page_table == nullptr ||
-                      (d->page_size >= kThreads * 8 / std::max(d->head_dim, 8) &&
-                       (d->page_size & (d->page_size - 1)) == 0 && d->max_pages > 0),
-                  "fdllm_kv_attn: page table needs a power-of-two page_size >= %d (got %d) and max_pages > 0",
-                  kThreads * 8 / std::max(d->head_dim, 8), d->page_size);
-  FDLLM_CHECK_ARG(d->kv_split >= 0 && d->kv_split % kKT == 0, "fdllm_kv_attn: kv_split %d not a multiple of %d",
-                  d->kv_split, kKT);
-  const int G = d->num_q_heads / d->num_kv_heads;
-  const int64_t R64 = static_cast<int64_t>(d->q_len) * G;
-  FDLLM_CHECK_ARG(R64 < (1 << 30), "fdllm_kv_attn: q_len * group too large");
-  pl->R = static_cast<int>(R64);
-  const int hkv = d->num_kv_heads;
-  const bool decode_shape = !(d->flags & FDLLM_ATTN_NO_DECODE_KERNEL) && d->head_dim == 128 && pl->R <= 64 &&
-                            (d->page_table == nullptr || d->page_size >= 32) &&
-                            d->k_stride_slot >= d->head_dim && d->v_stride_slot >= d->head_dim &&
-                            d->k_stride_slot < (1 << 24) && d->v_stride_slot < (1 << 24);
-  pl->kind = kPlanGeneral;
-  if (decode_shape && !(d->flags & FDLLM_ATTN_ALL_HEADS_DECODE)) {
-    const int max_len = d->page_table
-                            ? std::min<int64_t>(d->max_seqlen, static_cast<int64_t>(d->max_pages) * d->page_size)
-                            : d->max_seqlen;
-    const int64_t len = std::max(1, max_len);
-    const int64_t max_t = (len + 31) / 32;  // tiles of the longest sequence
-    // every split holds at most kDecodeMaxTiles tiles and a sequence at most kMaxDecodeSplits splits
-    if (max_t <= static_cast<int64_t>(kDecodeMaxTiles) * kMaxDecodeSplits &&
-        static_cast<int64_t>(d->batch) * hkv <= static_cast<int64_t>(kCounterBytes / sizeof(int))) {
-      const int64_t B = std::max(d->batch, 1);
-      const int64_t min_splits = (max_t + kDecodeMaxTiles - 1) / kDecodeMaxTiles;  // of the longest sequence
-      pl->kind = kPlanSplitDecode;
-      pl->decode = false;
-      pl->MT = 1;
-      pl->rows_per_wg = 64;
-      pl->n_rb = 1;
-      int64_t slots;  // partial slots per KV head
-      bool split_possible;
-      const bool pages_fit = d->page_table == nullptr || B * d->max_pages <= kBalMaxPages;
-      if (d->kv_split == 0 && B <= kBalancedMaxBatch && pages_fit && (d->flags & FDLLM_ATTN_BALANCED_SPLITS)) {
-        // pairs of 32-key tiles dealt evenly over S slots per KV head (S * Hkv ~ one
-        // workgroup per CU, S a multiple of 8 for the XCD-major slot order); partial
-        // slots S + batch per head (piece (s, b) owns slot s + b)
-        pl->kind = kPlanBalancedDecode;
-        pl->chunk = 0;
-        const int64_t s8 = std::max<int64_t>(8, (kSplitTargetWG / hkv + 7) / 8 * 8);
-        pl->n_splits = static_cast<int>(s8);
-        const int64_t pslots = s8 + B;
-        FDLLM_CHECK_ARG(pslots * hkv < (int64_t{1} << 31) / 64, "fdllm_kv_attn: too many split slots");
-        pl->ws_o_bytes = static_cast<size_t>(pslots) * hkv * 64 * d->head_dim * sizeof(float);
-        pl->ws_ml_bytes = static_cast<size_t>(pslots) * hkv * 64 * sizeof(float2);
-        return FDLLM_OK;
-      }
-      if (d->kv_split == 0 && B <= kBalancedMaxBatch) {
-        pl->chunk = 0;
-        slots = std::max<int64_t>((kSplitTargetWG + hkv - 1) / hkv, B * min_splits);
-        pl->n_splits = static_cast<int>(slots);
-        split_possible = slots > B;
-      } else {
-        int64_t chunk = d->kv_split > 0 ? d->kv_split : kSplitMaxChunk;
-        chunk = std::max<int64_t>(chunk, (max_t + kMaxDecodeSplits - 1) / kMaxDecodeSplits * 32);
-        chunk = std::min<int64_t>(chunk, kSplitMaxChunk);
-        pl->chunk = static_cast<int>(chunk);
-        pl->n_splits = static_cast<int>((max_t * 32 + chunk - 1) / chunk);  // per sequence
-        slots = B * pl->n_splits;
-        split_possible = pl->n_splits > 1;
-      }
-      FDLLM_CHECK_ARG(slots * hkv < (int64_t{1} << 31) / 64, "fdllm_kv_attn: too many split slots");
-      if (split_possible) {
-        pl->ws_o_bytes = static_cast<size_t>(slots) * hkv * 64 * d->head_dim * sizeof(float);
-        pl->ws_ml_bytes = static_cast<size_t>(slots) * hkv * 64 * sizeof(float2);
-      } else {
-        pl->ws_o_bytes = pl->ws_ml_bytes = 0;
-      }
-      return FDLLM_OK;
-    }
-  }
-  pl->decode = decode_shape && (hkv == 1 || hkv == 2 || hkv == 4 || hkv == 8) && d->k_stride_h == 128 &&
-               d->v_stride_h == 128;
-  if (pl->decode) {
-    pl->kind = kPlanAllHeads;
-    const int max_len = d->page_table
-                            ? std::min<int64_t>(d->max_seqlen, static_cast<int64_t>(d->max_pages) * d->page_size)
-                            : d->max_seqlen;
-    const int max_t32 = std::max(1, (max_len + 31) / 32);
-    int chunk_t32;
-    if (d->kv_split > 0) {
-      chunk_t32 = d->kv_split / 32;
-    } else {
-      // ~320 workgroups when every sequence is full length, >= 128 keys each
-      const int64_t splits = (320 + std::max(d->batch, 1) - 1) / std::max(d->batch, 1);
-      chunk_t32 = std::max<int>(4, static_cast<int>((max_t32 + splits - 1) / splits));
-    }
-    chunk_t32 = std::max(1, std::min(chunk_t32, max_t32));
-    pl->MT = 0;
-    pl->rows_per_wg = 64;
-    pl->n_rb = 1;
-    pl->chunk = chunk_t32 * 32;
-    pl->n_splits = (max_t32 + chunk_t32 - 1) / chunk_t32;
-    const int64_t units = static_cast<int64_t>(d->batch) * hkv;
-    if (pl->n_splits > 1) {
-      pl->ws_o_bytes = static_cast<size_t>(units) * pl->n_splits * 64 * d->head_dim * sizeof(float);
-      pl->ws_ml_bytes = static_cast<size_t>(units) * pl->n_splits * 64 * sizeof(float2);
-    } else {
-      pl->ws_o_bytes = pl->ws_ml_bytes = 0;
-    }
-    return FDLLM_OK;
-  }
-  // Block decode shapes (64 < rows per KV head <= 256, e.g. a whole 32-token block at
-  // GQA 7): the prefill kernel's math on one row block, keys split and merged as in the
-  // split decode kernel (64-key tiles)
-  const bool split_prefill_shape = !(d->flags & FDLLM_ATTN_NO_DECODE_KERNEL) && d->head_dim == 128 &&
-                                   pl->R > 64 && pl->R <= 256 && (d->kv_split == 0 || d->kv_split % 64 == 0) &&
-                                   (d->page_table == nullptr || d->page_size >= 32) &&
-                                   d->k_stride_slot < (1 << 24) && d->v_stride_slot < (1 << 24);
-  if (split_prefill_shape) {
-    const int max_len = d->page_table
-                            ? std::min<int64_t>(d->max_seqlen, static_cast<int64_t>(d->max_pages) * d->page_size)
-                            : d->max_seqlen;
-    const int64_t max_t = (std::max(1, max_len) + 63) / 64;  // 64-key tiles of the longest sequence
-    if (max_t <= static_cast<int64_t>(kDecodeMaxTiles) * kMaxDecodeSplits &&
-        static_cast<int64_t>(d->batch) * hkv <= static_cast<int64_t>(kCounterBytes / sizeof(int))) {
-      const int64_t B = std::max(d->batch, 1);
-      const int64_t min_splits = (max_t + kDecodeMaxTiles - 1) / kDecodeMaxTiles;
-      pl->kind = kPlanSplitPrefill;
-      pl->decode = false;
-      pl->MT = 4;
-      pl->rows_per_wg = 256;
-      pl->n_rb = 1;
-      int64_t slots;
-      bool split_possible;
-      if (d->kv_split == 0 && B <= kBalancedMaxBatch) {
-        pl->chunk = 0;
-        slots = std::max<int64_t>((kSplitTargetWG + hkv - 1) / hkv, B * min_splits);
-        pl->n_splits = static_cast<int>(slots);
-        split_possible = slots > B;
-      } else {
-        int64_t chunk = d->kv_split > 0 ? d->kv_split : static_cast<int64_t>(kDecodeMaxTiles) * 64;
-        chunk = std::max<int64_t>(chunk, (max_t + kMaxDecodeSplits - 1) / kMaxDecodeSplits * 64);
-        chunk = std::min<int64_t>(chunk, static_cast<int64_t>(kDecodeMaxTiles) * 64);
-        pl->chunk = static_cast<int>(chunk);
-        pl->n_splits = static_cast<int>((max_t * 64 + chunk - 1) / chunk);
-        slots = B * pl->n_splits;
-        split_possible = pl->n_splits > 1;
-      }
-      FDLLM_CHECK_ARG(slots * hkv < (int64_t{1} << 31) / 256, "fdllm_kv_attn: too many split slots");
-      if (split_possible) {
-        pl->ws_o_bytes = static_cast<size_t>(slots) * hkv * 256 * d->head_dim * sizeof(float);
-        pl->ws_unit_off = static_cast<size_t>(slots) * hkv * 256 * sizeof(float2);
-        pl->ws_ml_bytes = pl->ws_unit_off + static_cast<size_t>(B) * hkv * sizeof(int2);
-      } else {
-        pl->ws_o_bytes = pl->ws_ml_bytes = 0;
-      }
-      return FDLLM_OK;
-    }
-  }
-  // Prefill shapes: at least 8 row blocks of 256 per KV head, pages of >= 32 keys
-  const bool prefill_shape = !(d->flags & FDLLM_ATTN_NO_DECODE_KERNEL) && d->head_dim == 128 &&
-                             pl->R >= 8 * 256 && d->kv_split == 0 &&
-                             (d->page_table == nullptr || d->page_size >= 32) && d->k_stride_slot < (1 << 24) &&
-                             d->v_stride_slot < (1 << 24) && (pl->R + 255) / 256 < 65536;
-  if (prefill_shape) {
-    pl->kind = kPlanPrefill;
-    pl->MT = 4;
-    pl->rows_per_wg = 32 * kPrefillWaves;
-    pl->n_rb = (pl->R + pl->rows_per_wg - 1) / pl->rows_per_wg;
-    pl->n_splits = 1;
-    pl->chunk = 1 << 30;
-    pl->ws_o_bytes = pl->ws_ml_bytes = 0;
-    return FDLLM_OK;
-  }
-  const int mtiles = (pl->R + 15) / 16;
-  pl->MT = mtiles <= 4 ? 1 : (mtiles <= 8 ? 2 : 4);
-  pl->rows_per_wg = 64 * pl->MT;
-  pl->n_rb = (pl->R + pl->rows_per_wg - 1) / pl->rows_per_wg;
-  const int max_len = d->page_table ? std::min<int64_t>(d->max_seqlen, static_cast<int64_t>(d->max_pages) * d->page_size)
-                                    : d->max_seqlen;
-  const int max_tiles = std::max(1, (max_len + kKT - 1) / kKT);
-  int chunk_tiles;
-  if (d->kv_split > 0) {
-    chunk_tiles = d->kv_split / kKT;
-  } else {
-    // Aim for ~2 workgroups per CU (256 CUs) when every sequence is full length.
-    const int64_t units = static_cast<int64_t>(d->batch) * d->num_kv_heads * pl->n_rb;
-    const int64_t target = 512;
-    if (units >= target) {
-      chunk_tiles = max_tiles;
-    } else {
-      const int64_t splits = (target + units - 1) / std::max<int64_t>(units, 1);
-      chunk_tiles = static_cast<int>((max_tiles + splits - 1) / splits);
-      chunk_tiles = std::max(chunk_tiles, 4);  // >= 256 keys per split keeps partial traffic small
-    }
-  }
-  chunk_tiles = std::max(1, std::min(chunk_tiles, max_tiles));
-  const int64_t units = static_cast<int64_t>(d->batch) * d->num_kv_heads * pl->n_rb;
-  pl->chunk = chunk_tiles * kKT;
-  pl->n_splits = (max_tiles + chunk_tiles - 1) / chunk_tiles;
-  if (pl->n_splits > 1) {
-    pl->ws_o_bytes = static_cast<size_t>(units) * pl->n_splits * pl->rows_per_wg * d->head_dim * sizeof(float);
-    pl->ws_ml_bytes = static_cast<size_t>(units) * pl->n_splits * pl->rows_per_wg * sizeof(float2);
-  } else {
-    pl->ws_o_bytes = pl->ws_ml_bytes = 0;
-  }
-  return FDLLM_OK;
-}
-
-inline size_t align256(size_t x) { return (x + 255) & ~static_cast<size_t>(255); }
+inline dim3 to_dim3(const GridDims& g) { return dim3(g.x, g.y, g.z); }
 
 template <int D, bool F16, bool PAGED>
-void launch_combine(const AttnParams& p, unsigned units, hipStream_t s) {
-  const int rpb = 256 / (D / 8);
-  const dim3 cgrid((p.rows_per_wg + rpb - 1) / rpb, units);
+void launch_combine(const AttnParams& p, dim3 cgrid, hipStream_t s) {
   kv_attn_combine_kernel<D, F16, PAGED><<<cgrid, dim3(256), 0, s>>>(p);
 }
 
@@ -3646,9 +3371,9 @@ void launch_prefill(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
 }
 
 template <int HKV>
-void launch_decode(const AttnParams& p, bool f16, hipStream_t s) {
+void launch_decode(const AttnParams& p, bool f16, const LaunchSet& ls, hipStream_t s) {
   const bool paged = p.page_table != nullptr;
-  const dim3 grid(p.n_splits, p.B);
+  const dim3 grid = to_dim3(ls.main_grid);
   const dim3 block(128 * HKV);
   if (f16) {
     if (paged) kv_decode_kernel<HKV, true, true><<<grid, block, 0, s>>>(p);
@@ -3657,21 +3382,22 @@ void launch_decode(const AttnParams& p, bool f16, hipStream_t s) {
     if (paged) kv_decode_kernel<HKV, false, true><<<grid, block, 0, s>>>(p);
     else kv_decode_kernel<HKV, false, false><<<grid, block, 0, s>>>(p);
   }
-  if (p.n_splits > 1) {
-    const unsigned units = static_cast<unsigned>(p.B * HKV);
+  if (ls.second) {
+    const dim3 cgrid = to_dim3(ls.second_grid);
     if (f16) {
-      if (paged) launch_combine<128, true, true>(p, units, s);
-      else launch_combine<128, true, false>(p, units, s);
+      if (paged) launch_combine<128, true, true>(p, cgrid, s);
+      else launch_combine<128, true, false>(p, cgrid, s);
     } else {
-      if (paged) launch_combine<128, false, true>(p, units, s);
-      else launch_combine<128, false, false>(p, units, s);
+      if (paged) launch_combine<128, false, true>(p, cgrid, s);
+      else launch_combine<128, false, false>(p, cgrid, s);
     }
   }
 }
 
 template <int D, int MT>
-void launch_attn(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
+void launch_attn(const AttnParams& p, bool f16, const LaunchSet& ls, hipStream_t s) {
   const bool paged = p.page_table != nullptr;
+  const dim3 grid = to_dim3(ls.main_grid);
   if (f16) {
     if (paged) kv_attn_kernel<D, MT, true, true><<<grid, dim3(kThreads), 0, s>>>(p);
     else kv_attn_kernel<D, MT, true, false><<<grid, dim3(kThreads), 0, s>>>(p);
@@ -3679,29 +3405,16 @@ void launch_attn(const AttnParams& p, bool f16, dim3 grid, hipStream_t s) {
     if (paged) kv_attn_kernel<D, MT, false, true><<<grid, dim3(kThreads), 0, s>>>(p);
     else kv_attn_kernel<D, MT, false, false><<<grid, dim3(kThreads), 0, s>>>(p);
   }
-  if (p.n_splits > 1) {
-    const int rpb = 256 / (D / 8);
-    const dim3 cgrid((p.rows_per_wg + rpb - 1) / rpb, grid.y * grid.z);
+  if (ls.second) {
+    const dim3 cgrid = to_dim3(ls.second_grid);
     if (f16) {
-      if (paged) kv_attn_combine_kernel<D, true, true><<<cgrid, dim3(256), 0, s>>>(p);
-      else kv_attn_combine_kernel<D, true, false><<<cgrid, dim3(256), 0, s>>>(p);
+      if (paged) launch_combine<D, true, true>(p, cgrid, s);
+      else launch_combine<D, true, false>(p, cgrid, s);
     } else {
-      if (paged) kv_attn_combine_kernel<D, false, true><<<cgrid, dim3(256), 0, s>>>(p);
-      else kv_attn_combine_kernel<D, false, false><<<cgrid, dim3(256), 0, s>>>(p);
+      if (paged) launch_combine<D, false, true>(p, cgrid, s);
+      else launch_combine<D, false, false>(p, cgrid, s);
     }
   }
-}
-
-// Workspace layout: a fixed 64 KiB of arrival counters (one int per (sequence,
-// KV head)), the (m, l) pairs of every split partial (for the split prefill kernel
-// followed by its table of (first slot, splits) per (sequence, KV head)), then the
-// partial rows. The counter region has the same place and size for every call, so
-// partials of one call never land where a later call with more sequences keeps its
-// counters.
-inline size_t counter_bytes(const fdllm_kv_attn_desc*) { return kCounterBytes; }
-
-inline size_t plan_workspace_bytes(const fdllm_kv_attn_desc* d, const Plan& pl) {
-  return pl.ws_o_bytes > 0 ? counter_bytes(d) + align256(pl.ws_ml_bytes) + pl.ws_o_bytes : 0;
 }
 
 }  // namespace
@@ -3734,23 +3447,12 @@ uint64_t* g_timeline = nullptr;  // device buffer of the phase stamps (instrumen
 int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace, size_t workspace_bytes,
                    void* stream) {
   if (d->batch == 0 || d->q_len == 0) return FDLLM_OK;
-  FDLLM_CHECK_ARG(d->q && d->k && d->v && d->out && d->seqlens, "fdllm_kv_attn_fwd: null pointer");
-  FDLLM_CHECK_ARG(aligned16(d->q) && aligned16(d->k) && aligned16(d->v) && aligned16(d->out),
-                  "fdllm_kv_attn_fwd: q/k/v/out must be 16-byte aligned");
-  FDLLM_CHECK_ARG(d->q_stride_b % 8 == 0 && d->q_stride_s % 8 == 0 && d->q_stride_h % 8 == 0 &&
-                      d->k_stride_page % 8 == 0 && d->k_stride_slot % 8 == 0 && d->k_stride_h % 8 == 0 &&
-                      d->v_stride_page % 8 == 0 && d->v_stride_slot % 8 == 0 && d->v_stride_h % 8 == 0 &&
-                      d->out_stride_b % 8 == 0 && d->out_stride_s % 8 == 0 && d->out_stride_h % 8 == 0,
-                  "fdllm_kv_attn_fwd: strides must be multiples of 8 elements");
+  int rc = validate_call(d, pl, workspace, workspace_bytes);
+  if (rc != FDLLM_OK) return rc;
+  LaunchSet ls;
+  rc = plan_launches(d, pl, &ls);
+  if (rc != FDLLM_OK) return rc;
   const size_t need = plan_workspace_bytes(d, pl);
-  if (need > 0) {
-    if (workspace == nullptr || workspace_bytes < need || !aligned16(workspace)) {
-      set_last_error("fdllm_kv_attn_fwd: workspace of %zu bytes required (got %zu)", need, workspace_bytes);
-      return FDLLM_ERR_WORKSPACE;
-    }
-  }
-  const int64_t grid_z = static_cast<int64_t>(d->batch) * d->num_kv_heads;
-  FDLLM_CHECK_ARG(grid_z < 65536 && pl.n_rb < 65536, "fdllm_kv_attn_fwd: grid too large");
 
   AttnParams p;
   p.q = static_cast<const uint16_t*>(d->q);
@@ -3790,8 +3492,6 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
   p.mask_mode = d->mask_mode;
   p.mask_block = d->mask_block > 0 ? d->mask_block : 1;
   p.scale_log2 = d->softmax_scale * 1.4426950408889634f;
-  FDLLM_CHECK_ARG((d->k_new == nullptr) == (d->v_new == nullptr),
-                  "fdllm_kv_attn_fwd: k_new and v_new must both be given or both be NULL");
   p.kn = static_cast<const uint16_t*>(d->k_new);
   p.vn = static_cast<const uint16_t*>(d->v_new);
   p.n_sb = d->new_stride_b;
@@ -3803,16 +3503,10 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
 #if FDLLM_TIMELINE
   p.tl = g_timeline;
 #endif
-  if (p.kn != nullptr) {
-    FDLLM_CHECK_ARG(aligned16(d->k_new) && aligned16(d->v_new) && d->new_stride_b % 8 == 0 &&
-                        d->new_stride_s % 8 == 0 && d->new_stride_h % 8 == 0,
-                    "fdllm_kv_attn_fwd: k_new / v_new must be 16-byte aligned with strides in multiples of 8");
-    FDLLM_CHECK_ARG(d->new_stride_s < (1 << 24), "fdllm_kv_attn_fwd: new_stride_s too large");
-  }
   if (need > 0) {
     char* w = static_cast<char*>(workspace);
     p.ws_cnt = reinterpret_cast<int*>(w);
-    w += counter_bytes(d);
+    w += kCounterBytes;
     p.ws_ml = reinterpret_cast<float2*>(w);
     p.ws_o = reinterpret_cast<float*>(w + align256(pl.ws_ml_bytes));
     p.ws_unit = pl.kind == kPlanSplitPrefill ? reinterpret_cast<int2*>(w + pl.ws_unit_off) : nullptr;
@@ -3826,11 +3520,7 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (pl.kind == kPlanF32) {
     // 4 FDLLM_F32_ROWS_PER_WAVE rows of one (sequence, KV head) per workgroup
-    constexpr int rwg = 4 * FDLLM_F32_ROWS_PER_WAVE;
-    const int64_t rows = static_cast<int64_t>(d->q_len) * (d->num_q_heads / d->num_kv_heads);
-    FDLLM_CHECK_ARG(d->batch < 65536, "fdllm_kv_attn_fwd: batch too large");
-    const dim3 grid(static_cast<unsigned>((rows + rwg - 1) / rwg), static_cast<unsigned>(d->num_kv_heads),
-                    static_cast<unsigned>(d->batch));
+    const dim3 grid = to_dim3(ls.main_grid);
     const bool paged = d->page_table != nullptr;
     if (d->head_dim == 128) {
       if (paged) kv_attn_f32_kernel<2, true><<<grid, dim3(256), 0, s>>>(p);
@@ -3842,17 +3532,11 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }
   // Cache write of the call (k_new / v_new): inside the prefill kernels, otherwise (and
-  // with FDLLM_ATTN_CACHE_WRITE_KERNEL) as a kernel of its own before the attention, at
-  // q_start[b] + t (seqlens[b] - q_len + t). On the 4 x 4096-token prefill, timed in
-  // rotation: 473-475 us in-kernel against 479-480 us with the copy kernel.
-  // The prefill kernels read every key at or past the query start from the new rows,
-  // which is exact only when no visible key lies past the last new row. Without q_start
-  // that holds by construction (query start = visible length - q_len); an explicit
-  // q_start may leave visible cache rows past q_start + q_len, so such calls take the
-  // copy kernel, which stores the rows before the attention reads the cache.
-  const bool fuse_write = p.kn != nullptr && p.q_start == nullptr && !(d->flags & FDLLM_ATTN_CACHE_WRITE_KERNEL) &&
-                          (pl.kind == kPlanPrefill || pl.kind == kPlanSplitPrefill);
-  if (p.kn != nullptr && !fuse_write) {
+  // with FDLLM_ATTN_CACHE_WRITE_KERNEL or an explicit q_start) as a kernel of its own
+  // before the attention, at q_start[b] + t (seqlens[b] - q_len + t). On the 4 x 4096-token
+  // prefill, timed in rotation: 473-475 us in-kernel against 479-480 us with the copy kernel.
+  const bool fuse_write = plan_fuses_cache_write(d, pl);
+  if (ls.write) {
     KVWriteArgs a;
     a.k_new = p.kn;
     a.v_new = p.vn;
@@ -3861,8 +3545,6 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
     a.n_sh = p.n_sh;
     a.k_cache = const_cast<uint16_t*>(p.k);
     a.v_cache = const_cast<uint16_t*>(p.v);
-    FDLLM_CHECK_ARG(p.k_sp == p.v_sp && p.k_ss == p.v_ss && p.k_sh == p.v_sh,
-                    "fdllm_kv_attn_fwd: a cache write with this shape needs equal K and V cache strides");
     a.c_sp = p.k_sp;
     a.c_ss = p.k_ss;
     a.c_sh = p.k_sh;
@@ -3878,12 +3560,11 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
     a.T = p.Sq;
     a.Hkv = p.Hkv;
     a.D = d->head_dim;
-    const int64_t n = static_cast<int64_t>(a.B) * a.T * a.Hkv * (a.D / 8);
-    kv_write_kernel<<<dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s>>>(a);
+    kv_write_kernel<<<to_dim3(ls.write_grid), dim3(256), 0, s>>>(a);
   }
   if (pl.kind == kPlanBalancedDecode) {
     const bool paged = p.page_table != nullptr;
-    const dim3 grid(pl.n_splits, d->num_kv_heads);
+    const dim3 grid = to_dim3(ls.main_grid);
     if (f16) {
       if (paged) kv_balanced_decode_kernel<true, true><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
       else kv_balanced_decode_kernel<true, false><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
@@ -3895,7 +3576,7 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
   }
   if (pl.kind == kPlanSplitDecode) {
     const bool paged = p.page_table != nullptr;
-    const dim3 grid(pl.n_splits, d->num_kv_heads, pl.chunk > 0 ? d->batch : 1);
+    const dim3 grid = to_dim3(ls.main_grid);
     if (f16) {
       if (paged) kv_split_decode_kernel<kDecodeStages, true, true><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
       else kv_split_decode_kernel<kDecodeStages, true, false><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
@@ -3906,18 +3587,18 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }
   if (pl.kind == kPlanPrefill) {
-    const dim3 grid(static_cast<unsigned>(grid_z), pl.n_rb);
+    const dim3 grid = to_dim3(ls.main_grid);
     if (fuse_write) launch_prefill<false, true>(p, f16, grid, s);
     else launch_prefill<false, false>(p, f16, grid, s);
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }
   if (pl.kind == kPlanSplitPrefill) {
-    const dim3 grid(pl.n_splits, d->num_kv_heads, pl.chunk > 0 ? d->batch : 1);
+    const dim3 grid = to_dim3(ls.main_grid);
     if (fuse_write) launch_prefill<true, true>(p, f16, grid, s);
     else launch_prefill<true, false>(p, f16, grid, s);
-    if (p.ws_unit != nullptr) {
-      // units = B * Hkv; 32 rows per workgroup
-      const dim3 mgrid(static_cast<unsigned>((pl.R + 31) / 32), static_cast<unsigned>(d->batch * d->num_kv_heads));
+    if (ls.second) {
+      // one workgroup row per (sequence, KV head); 32 rows per workgroup
+      const dim3 mgrid = to_dim3(ls.second_grid);
       if (f16) kv_split_prefill_merge_kernel<true><<<mgrid, dim3(256), 0, s>>>(p);
       else kv_split_prefill_merge_kernel<false><<<mgrid, dim3(256), 0, s>>>(p);
     }
@@ -3925,22 +3606,21 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
   }
   if (pl.decode) {
     switch (d->num_kv_heads) {
-      case 1: launch_decode<1>(p, f16, s); break;
-      case 2: launch_decode<2>(p, f16, s); break;
-      case 4: launch_decode<4>(p, f16, s); break;
-      default: launch_decode<8>(p, f16, s); break;
+      case 1: launch_decode<1>(p, f16, ls, s); break;
+      case 2: launch_decode<2>(p, f16, ls, s); break;
+      case 4: launch_decode<4>(p, f16, ls, s); break;
+      default: launch_decode<8>(p, f16, ls, s); break;
     }
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }
-  const dim3 grid(pl.n_splits, pl.n_rb, static_cast<unsigned>(grid_z));
   if (d->head_dim == 128) {
-    if (pl.MT == 1) launch_attn<128, 1>(p, f16, grid, s);
-    else if (pl.MT == 2) launch_attn<128, 2>(p, f16, grid, s);
-    else launch_attn<128, 4>(p, f16, grid, s);
+    if (pl.MT == 1) launch_attn<128, 1>(p, f16, ls, s);
+    else if (pl.MT == 2) launch_attn<128, 2>(p, f16, ls, s);
+    else launch_attn<128, 4>(p, f16, ls, s);
   } else {
-    if (pl.MT == 1) launch_attn<64, 1>(p, f16, grid, s);
-    else if (pl.MT == 2) launch_attn<64, 2>(p, f16, grid, s);
-    else launch_attn<64, 4>(p, f16, grid, s);
+    if (pl.MT == 1) launch_attn<64, 1>(p, f16, ls, s);
+    else if (pl.MT == 2) launch_attn<64, 2>(p, f16, ls, s);
+    else launch_attn<64, 4>(p, f16, ls, s);
   }
   FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
 }

@@ -193,18 +193,7 @@ __device__ __forceinline__ void lds_barrier() {
 // ---------------------------------------------------------------------------
 // Host-side error plumbing shared by the C-ABI entry points.
 // ---------------------------------------------------------------------------
-namespace fdllm {
-void set_last_error(const char* fmt, ...);
-int dtype_size(int dtype);  // bytes per element of an FDLLM_DTYPE_*, 0 if unknown
-}
-
-#define FDLLM_CHECK_ARG(cond, ...)          \
-  do {                                      \
-    if (!(cond)) {                          \
-      ::fdllm::set_last_error(__VA_ARGS__); \
-      return FDLLM_ERR_INVALID_ARGUMENT;    \
-    }                                       \
-  } while (0)
+#include "host_errors.h"
 
 #define FDLLM_RETURN_LAUNCH_STATUS(what)                                            \
   do {                                                                              \
