@@ -319,3 +319,100 @@ def test_generation_with_confident_model(gpu):
     rate = _forced_rate(model, x, N, True, rec, rule, EagerStaticAttention())
     print(f"confident model: teacher-forced agreement with the fp32 oracle {rate:.4f}")
     assert rate >= 0.95
+
+
+@pytest.mark.timeout(900)
+def test_forward_numerics_7b_bs16(gpu, capsys):
+    """One full-block and one sub-block diffusion forward of the end-to-end workload's
+    model (28 layers, hidden 3584, 28 / 4 heads, random weights, batch 16) after a
+    512-token prefill, on the HIP path (attention kernels, HIP cache writes, fused
+    norms) and on the float32 eager oracle (oracle/e2e_eager.py); both with the block
+    cache, the full-block forward writing it and the sub-block forward (rows 8..15 of
+    the block, replace_position 8) reading it. Compared: the logits and every layer's
+    attention output (the self-attention module's output, after o_proj), as relative
+    errors ||x - oracle|| / ||oracle||.
+
+    With random weights, any bf16-level difference in one layer grows through the
+    residual stream of the layers after it, so the per-layer errors rise with depth even
+    without a mistake. The noise floor of that growth is measured in the same run: the
+    oracle with its attention probabilities rounded to bf16 before the PV product (the
+    rounding point of the kernels and of flash-attn, nothing else changed) against the
+    float32 oracle. Bars: layer 0 (identical inputs on both paths) below 5e-3, about one
+    bf16 rounding; at every layer and for the logits, the HIP path's error at most 1.25
+    times the floor's plus 2e-3. A wrong mask, head map, cache row or scale gives errors
+    of order one at the layer where it occurs. All errors are printed. (Measured on
+    MI355X: logits 4.59e-2 full-block / 4.56e-2 sub-block against a floor of 4.53e-2 /
+    4.54e-2; every layer within 3 % of the floor, from 2.8e-3 at layer 0 to 7.4e-2 at
+    layer 27; greedy agreement with the fp32 oracle 0.877 / 0.867, floor 0.877 / 0.836.)"""
+    cfg = em.BlockDiffusionConfig()
+    model = em.build_model(cfg, gpu)
+    B, P, BS, SB = 16, 512, cfg.bd_size, 8
+    mask_id = cfg.vocab_size - 1
+    g = torch.Generator().manual_seed(7)
+    prompt = torch.randint(0, cfg.vocab_size - 1, (B, P), generator=g).to(gpu)
+    block = torch.full((B, BS), mask_id, dtype=torch.long)
+    block[:, 0] = torch.randint(0, cfg.vocab_size - 1, (B,), generator=g)
+    block[:, 1:SB] = torch.randint(0, cfg.vocab_size - 1, (B, SB - 1), generator=g)  # a decoded first sub-block
+    block = block.to(gpu)
+    pos = torch.arange(P, P + BS, device=gpu)
+
+    def say(msg):
+        with capsys.disabled():
+            print(f"\n[forward numerics 7B bs16] {msg}", flush=True)
+
+    results = []
+    for impl in (es.HipStaticAttention(graphs=False), EagerStaticAttention(), EagerStaticAttention(p_bf16=True)):
+        cache, bcache = impl.make_caches(B, 1024, cfg, torch.bfloat16, gpu, True)
+        orig = impl.patch(model, bcache)
+        captured = {}
+        hooks = []
+        for i, layer in enumerate(model.model.layers):
+            def hook(mod, args, out, i=i):
+                o = out[0] if isinstance(out, tuple) else out
+                captured[i] = o.detach().float().clone()
+            hooks.append(layer.self_attn.register_forward_hook(hook))
+        try:
+            with torch.no_grad():
+                model(prompt, cache, update_past_key_values=True)
+                bcache.reset()
+                cache.set_kv_write_start(P)
+                cache.set_scratch_seqlens(P + BS)
+                cache.prepare_write_idx(BS)
+                captured.clear()
+                full = model(block, cache, use_block_cache=True, block_past_key_values=bcache, cache_position=pos,
+                             logits_to_keep=BS).float()
+                attn_full = [captured[i] for i in range(cfg.num_hidden_layers)]
+                assert len(bcache) == cfg.num_hidden_layers  # every layer wrote its block rows
+                captured.clear()
+                sub = model(block[:, SB:2 * SB], cache, use_block_cache=True, block_past_key_values=bcache,
+                            replace_position=SB, cache_position=pos[SB:2 * SB], logits_to_keep=SB).float()
+                attn_sub = [captured[i] for i in range(cfg.num_hidden_layers)]
+        finally:
+            for h in hooks:
+                h.remove()
+            impl.unpatch(model, orig)
+        torch.cuda.synchronize()
+        assert torch.isfinite(full).all() and torch.isfinite(sub).all()
+        results.append((full, attn_full, sub, attn_sub))
+        say(f"{impl.name}{' (bf16 P)' if getattr(impl, 'p_bf16', False) else ''}: done")
+
+    def rel(a, b):
+        return ((a - b).norm() / b.norm()).item()
+    hip, ref, floor = results
+    fails = []
+    for k, name in ((0, "full-block"), (2, "sub-block")):
+        lh, lf = rel(hip[k], ref[k]), rel(floor[k], ref[k])
+        eh = [rel(a, b) for a, b in zip(hip[k + 1], ref[k + 1])]
+        ef = [rel(a, b) for a, b in zip(floor[k + 1], ref[k + 1])]
+        say(f"{name} logits: HIP {lh:.3e}, floor {lf:.3e}; greedy agreement with the fp32 oracle: HIP "
+            f"{(hip[k].argmax(-1) == ref[k].argmax(-1)).float().mean():.4f}, floor "
+            f"{(floor[k].argmax(-1) == ref[k].argmax(-1)).float().mean():.4f}")
+        say(f"{name} attention output per layer, HIP / floor: " +
+            ", ".join(f"{i}: {a:.2e}/{b:.2e}" for i, (a, b) in enumerate(zip(eh, ef))))
+        if eh[0] >= 5e-3:
+            fails.append(f"{name} layer 0: {eh[0]:.3e}")
+        fails += [f"{name} layer {i}: {a:.3e} vs floor {b:.3e}" for i, (a, b) in enumerate(zip(eh, ef))
+                  if a > 1.25 * b + 2e-3]
+        if lh > 1.25 * lf + 2e-3:
+            fails.append(f"{name} logits: {lh:.3e} vs floor {lf:.3e}")
+    assert not fails, fails
