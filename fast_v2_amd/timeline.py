@@ -57,8 +57,11 @@ def analyse(st):
     st = st[ran]
     t0 = st[:, 0].min()
     rel = (st - t0).astype(np.float64) * TICK_US
-    active = st[:, 3] != 0
-    merged = st[:, 5] != 0
+    # a stamp counts only when written after the workgroup's own start in this call: with
+    # --back-to-back the buffer is cleared once before the N calls, and a workgroup that
+    # merged in an earlier call but not in the last keeps that call's (earlier) stamp
+    active = (st[:, 3] != 0) & (st[:, 3] >= st[:, 0])
+    merged = (st[:, 5] != 0) & (st[:, 5] >= st[:, 0])
     info = st[:, 6]
     ntiles = (info & 0xFFFF)[active]
     res = {"workgroups": int(ran.sum()), "active": int(active.sum()), "merging": int(merged.sum()),
