@@ -81,9 +81,9 @@ class ForwardGraphs:
     device memory: the token ids and positions are copied into the graph's static
     inputs before each replay, and the static cache's write position and visible
     lengths live in device tensors (StaticKVCache.kv_write_start / scratch_seqlens).
-    Commits and the prompt prefill are kinds of their own (the full block, or the
-    prompt, without the block cache); the host only advances the committed length
-    after the replay. The first use of a kind runs
+    Commits are a kind of their own (the full block without the block cache); the host
+    only advances the committed length after the replay. (The prompt prefill runs
+    eagerly in the same form: it runs once per generation.) The first use of a kind runs
     it eagerly once (on the capture stream, so allocations and the attention
     workspace exist before capture), captures it, and replays it; the eager run and
     the replay write the same cache rows."""
@@ -193,18 +193,16 @@ def generate(model, input_ids: torch.Tensor, max_new_tokens: int = 1024, block_s
         if min_len > block_size:
             prefill_len = min_len // block_size * block_size
             if graphs is not None and isinstance(cache, StaticKVCache) and cache.get_seq_length() == 0:
-                # replayed from its own graph, as the commits are: the prompt's rows written
-                # at kv_write_start = 0, every prompt key visible as in the eager call, the
-                # last position's logits kept (the only ones read); the committed length
-                # then advances on the host
+                # the commits' form of the forward (the prompt's rows written at
+                # kv_write_start = 0, every prompt key visible as in the update path, the last
+                # position's logits kept, the only ones read; the committed length then
+                # advances on the host), run eagerly: it runs once per generation, where a
+                # graph would cost an eager run and a capture for a single replay
                 cache.set_kv_write_start(0)
                 cache.set_scratch_seqlens(prefill_len)
                 cache.prepare_write_idx(prefill_len)
-
-                def prefill_fwd(ids, pos):
-                    return model(ids, cache, cache_position=pos, logits_to_keep=1)
-                logits = graphs(("prefill", prefill_len), prefill_fwd, x[:, :prefill_len],
-                                torch.arange(prefill_len, device=dev))
+                logits = model(x[:, :prefill_len], cache, cache_position=torch.arange(prefill_len, device=dev),
+                               logits_to_keep=1)
                 cache.commit_written(prefill_len)
             else:
                 logits = model(x[:, :prefill_len], cache, update_past_key_values=True)

@@ -44,9 +44,11 @@ Pinning status (what checks each function; see tests/test_oracle_*.py):
   e2e_eager                         pinned through its parts: its float32
                                     attention equals attention.sdpa_kvcache (and
                                     the one-key closed form); its caches' writes
-                                    equal cache_write_np. Projections and RoPE are
-                                    plain torch ops in the reference's order:
-                                    parity unpinned for the layer beyond these parts
+                                    equal cache_write_np; its RoPE equals the
+                                    explicit pairwise rotation (identity at
+                                    position 0, norms kept, relative positions).
+                                    The projections are the model's own nn.Linear
+                                    modules, applied in the reference's order
 There are no golden vectors in the reference (its tests generate inputs from
 seeds on CUDA), and no function here needed an import of the reference.
 """

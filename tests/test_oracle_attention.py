@@ -327,3 +327,38 @@ def test_e2e_oracle_caches_follow_the_static_cache_rules():
     before = bc.key_cache[2].clone()
     bc.write(kb, kb, 2, 16)
     np.testing.assert_array_equal(bc.key_cache[2].numpy(), oa.cache_write_np(before.numpy(), kb.numpy(), [16, 16]))
+
+
+def test_e2e_oracle_rope_is_the_pairwise_rotation():
+    """The eager oracle's RoPE, q * cos + rotate_half(q) * sin (modeling.py:168-200), is the
+    rotation of each pair (x_i, x_{i + D/2}) by the angle of its frequency:
+    (x cos t - y sin t, y cos t + x sin t), written out element by element here. Position 0
+    is the identity, norms are kept, and a dot product of a rotated query and key depends
+    only on the distance of their positions. A planted sign error in rotate_half fails the
+    explicit rotation."""
+    from oracle.e2e_eager import _rotate_half
+    g = torch.Generator().manual_seed(11)
+    D, P = 16, 9
+    x = torch.randn(P, D, generator=g, dtype=torch.float64)
+    inv_freq = 1.0 / (10000.0 ** (torch.arange(0, D, 2, dtype=torch.float64) / D))
+    ang = torch.arange(P, dtype=torch.float64)[:, None] * inv_freq[None, :]  # [P, D/2]
+    emb = torch.cat((ang, ang), dim=-1)
+    cos, sin = emb.cos(), emb.sin()
+    got = x * cos + _rotate_half(x) * sin
+    h = D // 2
+    exp = torch.empty_like(x)
+    for p in range(P):
+        for i in range(h):
+            c, s = math.cos(ang[p, i].item()), math.sin(ang[p, i].item())
+            exp[p, i] = x[p, i] * c - x[p, i + h] * s
+            exp[p, i + h] = x[p, i + h] * c + x[p, i] * s
+    torch.testing.assert_close(got, exp, atol=1e-12, rtol=0)
+    torch.testing.assert_close(got[0], x[0], atol=0, rtol=0)
+    torch.testing.assert_close(got.norm(dim=-1), x.norm(dim=-1), atol=1e-12, rtol=0)
+    q, k = torch.randn(D, generator=g, dtype=torch.float64), torch.randn(D, generator=g, dtype=torch.float64)
+
+    def rot(v, p):
+        return v * cos[p] + _rotate_half(v) * sin[p]
+    assert abs(rot(q, 5) @ rot(k, 2) - rot(q, 7) @ rot(k, 4)) < 1e-12
+    planted = x * cos + torch.cat((x[..., h:], -x[..., :h]), dim=-1) * sin
+    assert not torch.allclose(planted, exp)
