@@ -211,8 +211,8 @@ def bench_decode(torch, args):
     step(args.steps - 1)
     eager = out.clone()
     us = _time_graph(torch, step, args.steps, args.warmup)
-    if not args.no_check and not torch.equal(out, eager):
-        raise RuntimeError("graph replay output differs from the eager call")
+    if not torch.equal(out, eager):
+        raise RuntimeError("decode: graph replay output differs from the eager call")
     extra_layouts = {}
     if args.layout == "paged_hm":
         # the same values in token-major pages ([page_size, Hkv, D] per page, the paged layout
@@ -224,7 +224,13 @@ def bench_decode(torch, args):
             ops.block_attn(q, kt[i % layers], vt[i % layers], sl, wl.scale, page_table=pt, page_size=page_size,
                            out=out, kv_split=args.kv_split, balanced_splits=args.balanced_splits)
 
+        step_tm(args.steps - 1)
+        eager_tm = out.clone()
         extra_layouts["us_per_step_token_major_pages"] = _time_graph(torch, step_tm, args.steps, args.warmup)
+        if not torch.equal(out, eager_tm):
+            raise RuntimeError("decode (token-major pages): graph replay output differs from the eager call")
+        # the same values in the other page layout: the same arithmetic, so the same bits
+        extra_layouts["token_major_output_bit_identical"] = bool(torch.equal(eager_tm, eager))
         del kt, vt
         torch.cuda.empty_cache()
     # the practical floor of the call: a plain read of the same K/V bytes in the same tile
@@ -300,7 +306,12 @@ def bench_decode_full(torch, args):
         ops.block_attn(q, kp[i % layers], vp[i % layers], sl, wl.scale, page_table=pt,
                        page_size=wl.page_size, out=out)
 
+    # graph replay must reproduce the eager result bit for bit (both kernels of the step)
+    step(args.steps - 1)
+    eager = out.clone()
     us = _time_graph(torch, step, args.steps, args.warmup)
+    if not torch.equal(out, eager):
+        raise RuntimeError("full-block decode: graph replay output differs from the eager call")
     nbytes = workloads.decode_bytes(wl.seqlens, Hq, Hkv, D, Sq)
     flops = workloads.decode_flops(wl.seqlens, Hq, D, Sq)
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -510,7 +521,11 @@ def bench_small_fp32(torch, args):
 
     def step(i):
         ops.block_attn(q, k, v, sl, wl.scale, out=out)
+    step(0)
+    eager = out.clone()
     us = _time_graph(torch, step, 200, 4)
+    if not torch.equal(out, eager):
+        raise RuntimeError("fp32 attention: graph replay output differs from the eager call")
     flops = 4 * 32 * 12 * 128 * 544
     return {"us_per_call": us, "gflops": flops / (us * 1e-6) / 1e9,
             "workload": "fp32, q [1, 32, 12, 128] over 544 keys of 2 KV heads (kv_attn_f32_kernel)"}
@@ -618,7 +633,7 @@ def bench_e2e(torch, args):
            "tokens_per_step": round(sum(st.step_tokens) / max(len(st.step_tokens), 1), 3),
            "params": em.param_count(cfg), "model_build_s": round(build_s, 2),
            "gemm_tuning": "torch TunableOp over hipBLASLt / rocBLAS solutions, tuned in the warm-up",
-           "forwards_graphed": "prompt prefill, diffusion steps and commits replayed from HIP graphs",
+           "forwards_graphed": "diffusion steps and commits replayed from HIP graphs; the prompt prefill runs eagerly (once per generation)",
            "weights": args.e2e_weights or ("random init (N(0, 0.02), zero biases, unit norms) except the mask "
                                            "token's lm_head row, which is zero: a random model may otherwise "
                                            "predict the mask token, which the unmask rule writes back, and the "
@@ -808,7 +823,6 @@ def main() -> int:
     ap.add_argument("--layout", choices=["paged", "paged_hm", "contig", "bhsd"], default="paged_hm",
                     help="KV layout: 32-token pages (token-major), 32-token pages stored head-major, the "
                          "contiguous [B, max_S, Hkv, D] static cache, or the same cache stored head-major")
-    ap.add_argument("--no-check", action="store_true", help="skip the graph-vs-eager equality check")
     ap.add_argument("--balanced-splits", action="store_true",
                     help="decode: deal all sequences' keys evenly over the workgroups (runs across sequences)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -937,7 +951,8 @@ def main() -> int:
             "extra": {
                 "decode": {k: decode[k] for k in ("bytes_per_step", "flops_per_step", "tflops",
                                                   "us_per_model_step_28_layers", "layout",
-                                                  "us_per_step_token_major_pages", "ceiling") if k in decode},
+                                                  "us_per_step_token_major_pages",
+                                                  "token_major_output_bit_identical", "ceiling") if k in decode},
                 **extra,
             },
         }
