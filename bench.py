@@ -469,7 +469,7 @@ def bench_prefill(torch, args):
     out = torch.empty_like(q)
 
     def whole_call(i):
-        # the whole config-4 call: the K/V rows stored into the cache and the attention, in
+        # the whole 4 x 4096-token prefill call: the K/V rows stored into the cache and the attention, in
         # one fdllm_kv_attn_fwd (the prefill kernel stores the rows itself)
         ops.block_attn(q, kc, vc, sl, wl.scale, mask_mode=_ffi.MASK_BLOCK_CAUSAL, mask_block=wl.block, out=out,
                        k_new=k, v_new=v)
@@ -509,7 +509,7 @@ def bench_prefill(torch, args):
 
 
 def bench_small_fp32(torch, args):
-    """Config 1 on the GPU: the fp32 attention kernel on the fp32 workload (batch 1, 32
+    """The small fp32 decode on the GPU: the fp32 attention kernel on the fp32 workload (batch 1, 32
     queries x 12 / 2 heads over 512 + 32 keys, head_dim 128), the call as the caller
     makes it (one graph node per call)."""
     from fast_v2_amd import ops, workloads
@@ -740,7 +740,7 @@ def cpu_baseline_prefill(torch):
 
 
 def cpu_baseline_small_fp32(torch):
-    """Config 1 on the CPU: the SDPA shim in fp32, batch 1, 12 / 2 heads, 512 prefix + 32
+    """The small fp32 decode on the CPU: the SDPA shim in fp32, batch 1, 12 / 2 heads, 512 prefix + 32
     block keys, 32 queries (the reference's only CPU statement of the kv-cache attention)."""
     from fast_v2_amd import workloads
     from oracle import attention as oa
@@ -755,7 +755,7 @@ def cpu_baseline_small_fp32(torch):
 
 
 def cpu_baseline_e2e_step(torch):
-    """Config 5 on the CPU (the whole 7B model at batch 16 does not fit a bounded sample):
+    """The end-to-end generation step on the CPU (the whole 7B model at batch 16 does not fit a bounded sample):
     one decoder layer of the random-init 7B-layout model running a sub-block diffusion
     step (16 sequences x 8 tokens at positions 512..519, attention over the 512-token
     prompt plus the 32-token block through the SDPA shim, the reference's eager path
@@ -886,7 +886,7 @@ def main() -> int:
              f"{extra['scatter_rows']['achieved_gbs']:.0f} GB/s")
     if args.only is None:
         extra["small_fp32"] = bench_small_fp32(torch, args)
-        _log(f"small fp32 (config 1): {extra['small_fp32']['us_per_call']:.2f} us per call")
+        _log(f"small fp32 decode (batch 1, 12 / 2 heads, 544 keys): {extra['small_fp32']['us_per_call']:.2f} us per call")
     if args.only in (None, "prefill"):
         extra["prefill"] = bench_prefill(torch, args)
         _log(f"prefill: {extra['prefill']['us_per_call']:.1f} us per call with the cache write, "
@@ -903,9 +903,9 @@ def main() -> int:
 
     cpu = None
     if decode is not None and not args.no_cpu_baseline:
-        _log("cpu baseline (decode, config 3) ...")
+        _log("cpu baseline (bs16 sub-block decode step) ...")
         cpu = cpu_baseline_decode(torch, wl)
-        _log("cpu baseline (config 1, fp32 SDPA) ...")
+        _log("cpu baseline (small fp32 decode, SDPA shim) ...")
         extra["small_fp32_cpu"] = cpu_baseline_small_fp32(torch)
     if not args.no_cpu_baseline:
         if "gather_rmsnorm" in extra:

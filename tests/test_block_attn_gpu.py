@@ -46,7 +46,7 @@ def test_golden_small_decode_bf16(gpu):
 
 
 def test_golden_small_decode_fp32(gpu):
-    """Config 1 at its own precision: the fp32 golden (torch CPU SDPA, 1 x 32 queries x
+    """The small fp32 decode (batch 1, 12 / 2 heads, 512 + 32 keys) at its own precision: the fp32 golden (torch CPU SDPA, 1 x 32 queries x
     12/2 heads over 512 + 32 keys) against the fp32 kernel on the same fp32 inputs, within
     1e-5 (both accumulate in fp32; only the summation order differs)."""
     z = np.load(GOLDEN / "kv_decode_small.npz")
