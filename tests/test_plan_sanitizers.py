@@ -24,9 +24,10 @@ def test_planner_sweep_under_asan_ubsan(tmp_path):
            "-I", str(ROOT / "include"), "-I", str(ROOT / "fast_v2_amd" / "csrc"),
            str(ROOT / "tests" / "plan_sweep.cc"), "-o", str(exe)]
     subprocess.run(cmd, check=True, capture_output=True, text=True, timeout=300)
-    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0",
+    # verify_asan_link_order=0: the sanitizer runtime need not come first among the
+    # libraries the environment preloads
+    env = dict(os.environ, ASAN_OPTIONS="detect_leaks=1:abort_on_error=0:verify_asan_link_order=0",
                UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1")
-    env.pop("LD_PRELOAD", None)
     r = subprocess.run([str(exe)], capture_output=True, text=True, timeout=600, env=env)
     print(r.stdout)
     assert r.returncode == 0, r.stdout + r.stderr[-4000:]
