@@ -771,3 +771,33 @@ def test_fused_cache_write(gpu, case, in_kernel):
     vx = torch.from_numpy(exp_v).view(dtype) if dtype != torch.float16 else torch.from_numpy(exp_v)
     _check(out, oa.attention_np(q.float(), kx.float(), vx.float(), torch.clamp(sl, max=cap), mask_mode=mode,
                                 mask_block=blk, q_start=qst, page_table=pt, page_size=page or None))
+
+
+@pytest.mark.parametrize("B", [16000, 20000])
+@pytest.mark.parametrize("paged", [False, True])
+def test_large_batch_grid(gpu, B, paged):
+    """Thousands of sequences of one KV head (q_len 1, 0-96 visible keys). 16000: more
+    sequences than the per-sequence partition takes, so the split decode kernel runs with
+    fixed chunks on a grid whose third dimension is the batch; 20000: more (sequence, KV
+    head) pairs than the split kernel's arrival counters, so the all-heads decode kernel
+    takes the call on a grid whose second dimension is the batch. Within the bars of the
+    float64 oracle on a sample of 400 sequences; an empty sequence gives zero rows."""
+    print(f"case large batch B={B} paged={paged}", flush=True)
+    g = torch.Generator().manual_seed(23 + B)
+    Sq, Hq, Hkv, D, S = 1, 2, 1, 128, 96
+    q = torch.randn(B, Sq, Hq, D, generator=g).to(torch.bfloat16)
+    k = torch.randn(B, S, Hkv, D, generator=g).to(torch.bfloat16)
+    v = torch.randn(B, S, Hkv, D, generator=g).to(torch.bfloat16)
+    seqlens = torch.randint(0, S + 1, (B,), generator=g, dtype=torch.int32)
+    seqlens[:3] = torch.tensor([0, 1, S], dtype=torch.int32)
+    if paged:
+        kp, vp, pt = _paginate(k, v, 32, g)
+        out = ops.block_attn(q.to(gpu), kp.to(gpu), vp.to(gpu), seqlens.to(gpu), page_table=pt.to(gpu),
+                             page_size=32).cpu()
+    else:
+        out = ops.block_attn(q.to(gpu), k.to(gpu), v.to(gpu), seqlens.to(gpu)).cpu()
+    assert torch.count_nonzero(out[0]) == 0
+    # the oracle on a sample of the sequences (the kernel's grid covers all of them)
+    sel = torch.cat([torch.arange(3), torch.randperm(B - 3, generator=g)[:397] + 3])
+    exp = oa.attention_np(q[sel].float(), k[sel].float(), v[sel].float(), seqlens[sel])
+    _check(out[sel], exp)

@@ -332,3 +332,53 @@ def test_silu_mul_errors(gpu):
         ops.silu_mul(a, a.clone())
     with pytest.raises(RuntimeError):
         ops.silu_mul(torch.randn(8, device=gpu), torch.randn(8, device=gpu))
+
+
+def test_scatter_colliding_indices(gpu):
+    """Indices that repeat within a sequence (a collision): the reference kernel's writers
+    race (fused_gather_norm.cu:79-99), so each destination row must hold exactly one of the
+    value rows aimed at it, the same one in both destinations, and every other row keeps its
+    contents."""
+    g = torch.Generator().manual_seed(41)
+    B, S, T, H = 2, 16, 12, 256
+    vals = torch.randn(B, T, H, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, 5, (B, T), generator=g)  # rows 0-4 only: many collisions
+    cache = torch.randn(B, S, H, generator=g).to(torch.bfloat16)
+    cur = torch.randn(B, S, H, generator=g).to(torch.bfloat16)
+    c_gpu, u_gpu = cache.to(gpu), cur.to(gpu)
+    ops.scatter_rows(vals.to(gpu), idx.to(gpu), c_gpu, u_gpu)
+    c_out, u_out = c_gpu.cpu(), u_gpu.cpu()
+    for b in range(B):
+        for r in range(S):
+            src = [t for t in range(T) if int(idx[b, t]) == r]
+            if not src:
+                assert torch.equal(c_out[b, r], cache[b, r]) and torch.equal(u_out[b, r], cur[b, r])
+                continue
+            hits = [t for t in src if torch.equal(c_out[b, r], vals[b, t])]
+            assert hits, f"row {b},{r} holds none of its {len(src)} writers"
+            assert torch.equal(u_out[b, r], c_out[b, r])
+
+
+@pytest.mark.parametrize("H", [8, 64])
+def test_gather_and_scatter_large_batch(gpu, H):
+    """70000 sequences (more than a 65535-high grid dimension): the gather takes its generic
+    kernel and the scatter one row per workgroup; bit-exact rows, the norm within the bars."""
+    print(f"case large batch gather/scatter H={H}", flush=True)
+    g = torch.Generator().manual_seed(43 + H)
+    B, S, T = 70000, 3, 2
+    hidden = torch.randn(B, S, H, generator=g).to(torch.bfloat16)
+    idx = torch.randint(0, S, (B, T), generator=g)
+    w = (1 + 0.05 * torch.randn(H, generator=g)).to(torch.bfloat16)
+    normed, gathered = ops.gather_rmsnorm(hidden.to(gpu), idx.to(gpu), w.to(gpu), 1e-6,
+                                          og.NORM_WEIGHT_AFTER_CAST, True)
+    exp_g = torch.gather(hidden, 1, idx.unsqueeze(-1).expand(-1, -1, H))
+    assert torch.equal(gathered.cpu(), exp_g)
+    _, ref_n = og.ref_gather_input_rmsnorm(hidden, idx, w, 1e-6)
+    torch.testing.assert_close(normed.float().cpu(), ref_n.float(), atol=ATOL, rtol=RTOL)
+    vals = torch.randn(B, T, H, generator=g).to(torch.bfloat16)
+    sidx = torch.stack([torch.randperm(S, generator=g)[:T] for _ in range(64)]).repeat(B // 64 + 1, 1)[:B]
+    cache = hidden.clone()
+    c_gpu = cache.to(gpu)
+    ops.scatter_rows(vals.to(gpu), sidx.to(gpu), c_gpu)
+    exp_c = cache.clone().scatter_(1, sidx.unsqueeze(-1).expand(-1, -1, H), vals)
+    assert torch.equal(c_gpu.cpu(), exp_c)
