@@ -53,7 +53,9 @@ constexpr int kSc1 = 16;
 #ifndef FDLLM_DECODE_STAGES
 #define FDLLM_DECODE_STAGES 2
 #endif
-constexpr int kDecodeStages = FDLLM_DECODE_STAGES;  // tiles in flight per workgroup in the split decode kernel
+// tiles in flight per team in the split decode kernel: 2, or 3 (slower on the bs16 step:
+// 25.9 against 25.35 us, more loads in flight slow the phase in which every workgroup streams)
+constexpr int kDecodeStages = FDLLM_DECODE_STAGES;
 // 1: the balanced split kernels number their slots XCD-major (decode_partition); on the
 // bs16 sub-block decode step 27.27 us against 27.75 us in slot order.
 // 1: the split prefill (full-block) shapes also take kv_prefill_ring_kernel (bs16
@@ -1144,8 +1146,8 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
     u32x4 k[2];
     u32x4 v[2];
   };
-  static_assert(NS == 2, "two register stages (named, so both paths into the loop agree on registers)");
-  Stage st0, st1;
+  static_assert(NS == 2 || NS == 3, "two or three register stages (named, so both paths into the loop agree on registers)");
+  Stage st0, st1, st2;
 
   if constexpr (PAGED) __syncthreads();  // sPage visible
 
@@ -1255,16 +1257,18 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
     store_tile(sg, j & 1);
     lds_barrier();
     if (FDLLM_TIMELINE && j == 0) FDLLM_STAMP(2, __builtin_amdgcn_s_memrealtime());  // first tiles in LDS
-    load_tile(sg, j + 2);
+    load_tile(sg, j + NS);
     const int t = 2 * j + team;
     if (t < ntiles) compute_tile(j & 1, k_lo + t * KT);  // wave-uniform
   };
   if (nsteps > 0) {
     load_tile(st0, 0);
     load_tile(st1, 1);
-    for (int j = 0; j < nsteps; j += 2) {
+    if constexpr (NS == 3) load_tile(st2, 2);
+    for (int j = 0; j < nsteps; j += NS) {
       step(st0, j);
       step(st1, j + 1);
+      if constexpr (NS == 3) step(st2, j + 2);
     }
   }
 
