@@ -2732,6 +2732,10 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
 
   // Tile tt into slot `slot`: 2 K and 2 V loads per wave (4 more where a 32-key half
   // holds qs: each lane then loads from its own row's source under an exec mask).
+  // The SPLIT form reads each tile in one workgroup only and streams it (non-temporal:
+  // 46.46 -> 45.75 us per bs16 full-block step); the prefill form's row blocks of one
+  // (sequence, KV head) read the same tiles again from L2, so it keeps them cached
+  // (non-temporal there: 456 -> 472 us for the 4 x 4096 attention).
   // mode (a constant at every call site, so each loop copy below folds it away):
   // 0 every key from the cache, 1 every key from the new rows, 2 either, per half / lane
   auto issue = [&](int tt, int slot, const int mode) __attribute__((always_inline)) {
@@ -2743,20 +2747,20 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
       const int64_t noffs = static_cast<int64_t>(kh - qs) * p.n_ss;
       const i32x4 ks = make_srd(knbase + noffs, valid * nrow_bytes);
       const i32x4 vs = make_srd(vnbase + noffs, valid * nrow_bytes);
-      lds_dma16(ks, knso0, kd);
-      lds_dma16(vs, vnso0, vd);
-      lds_dma16(ks, knso1, kd + 1024);
-      lds_dma16(vs, vnso1, vd + 1024);
+      lds_dma16<SPLIT>(ks, knso0, kd);
+      lds_dma16<SPLIT>(vs, vnso0, vd);
+      lds_dma16<SPLIT>(ks, knso1, kd + 1024);
+      lds_dma16<SPLIT>(vs, vnso1, vd + 1024);
       return;
     }
     const int page = half_page(kh);
     if (mode == 0) {
       const i32x4 ks = make_srd(kbase + cache_off(page, kh, true), valid * krow_bytes);
       const i32x4 vs = make_srd(vbase + cache_off(page, kh, false), valid * vrow_bytes);
-      lds_dma16(ks, kso0, kd);
-      lds_dma16(vs, vso0, vd);
-      lds_dma16(ks, kso1, kd + 1024);
-      lds_dma16(vs, vso1, vd + 1024);
+      lds_dma16<SPLIT>(ks, kso0, kd);
+      lds_dma16<SPLIT>(vs, vso0, vd);
+      lds_dma16<SPLIT>(ks, kso1, kd + 1024);
+      lds_dma16<SPLIT>(vs, vso1, vd + 1024);
       return;
     }
     if (FUSED && kh < qs && qs < kh + 32 && valid > 0) {
@@ -2767,18 +2771,18 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
       // per lane: row key - qs of the new rows, or row key - kh of the cache rows
       const int d = (kh - qs) * nrow_bytes;  // shifts a new-row offset from half row hr to row kh + hr - qs
       if (kh + hrow0 >= qs) {
-        lds_dma16(kq, knso0 + d, kd);
-        lds_dma16(vq, vnso0 + d, vd);
+        lds_dma16<SPLIT>(kq, knso0 + d, kd);
+        lds_dma16<SPLIT>(vq, vnso0 + d, vd);
       } else {
-        lds_dma16(kc, kso0, kd);
-        lds_dma16(vc, vso0, vd);
+        lds_dma16<SPLIT>(kc, kso0, kd);
+        lds_dma16<SPLIT>(vc, vso0, vd);
       }
       if (kh + hrow1 >= qs) {
-        lds_dma16(kq, knso1 + d, kd + 1024);
-        lds_dma16(vq, vnso1 + d, vd + 1024);
+        lds_dma16<SPLIT>(kq, knso1 + d, kd + 1024);
+        lds_dma16<SPLIT>(vq, vnso1 + d, vd + 1024);
       } else {
-        lds_dma16(kc, kso1, kd + 1024);
-        lds_dma16(vc, vso1, vd + 1024);
+        lds_dma16<SPLIT>(kc, kso1, kd + 1024);
+        lds_dma16<SPLIT>(vc, vso1, vd + 1024);
       }
       return;
     }
@@ -2795,10 +2799,10 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
     // value selects (a conditional of two named ints is an lvalue: clang would select
     // their addresses and keep them in scratch memory)
     const int sel = from_new ? 1 : 0;
-    lds_dma16(ks, kso0 + sel * (knso0 - kso0), kd);
-    lds_dma16(vs, vso0 + sel * (vnso0 - vso0), vd);
-    lds_dma16(ks, kso1 + sel * (knso1 - kso1), kd + 1024);
-    lds_dma16(vs, vso1 + sel * (vnso1 - vso1), vd + 1024);
+    lds_dma16<SPLIT>(ks, kso0 + sel * (knso0 - kso0), kd);
+    lds_dma16<SPLIT>(vs, vso0 + sel * (vnso0 - vso0), vd);
+    lds_dma16<SPLIT>(ks, kso1 + sel * (knso1 - kso1), kd + 1024);
+    lds_dma16<SPLIT>(vs, vso1 + sel * (vnso1 - vso1), vd + 1024);
   };
 
   // ---- MFMA operand addresses (bytes from ring): K row 32 st + n32, chunk 2 ks + h;

@@ -152,7 +152,10 @@ __device__ __forceinline__ i32x4 make_srd(const void* base, int bytes) {
 // Direct-to-LDS load: 16 bytes per lane from buffer offset voff to LDS byte address
 // lds + 16 * lane (one 1 KB block per wave; lanes past the descriptor's size write
 // zeros without memory traffic). The compiler does not see the LDS write, so readers
-// wait with wait_vmcnt and a barrier; M0 is restored after the load.
+// wait with wait_vmcnt and a barrier; M0 is restored after the load. NT: the
+// non-temporal (streaming) policy, for data read once; without it the lines stay in L2
+// for other workgroups that read them again.
+template <bool NT = false>
 __device__ __forceinline__ void lds_dma16(i32x4 srd_in, int voff, uint32_t lds_in) {
   // both are wave-uniform by construction; readfirstlane puts them in scalar registers
   i32x4 srd;
@@ -160,13 +163,23 @@ __device__ __forceinline__ void lds_dma16(i32x4 srd_in, int voff, uint32_t lds_i
   for (int i = 0; i < 4; ++i) srd[i] = __builtin_amdgcn_readfirstlane(srd_in[i]);
   const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_in);
   int saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %3\n\t"
-      "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(voff), "s"(srd), "s"(lds));
+  if constexpr (NT) {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen nt lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(srd), "s"(lds));
+  } else {
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "buffer_load_dwordx4 %1, %2, 0 offen lds\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(voff), "s"(srd), "s"(lds));
+  }
 }
 
 // Wait until at most N vector memory operations of this wave are outstanding.
