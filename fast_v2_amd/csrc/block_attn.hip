@@ -3654,8 +3654,9 @@ __global__ __launch_bounds__(256) void zero_words_kernel(uint32_t* p, int n) {
 }
 
 // Device address of the current device's scratch. The first call on a device
-// resolves it with that device current and clears the counters on `stream`; it is
-// refused under stream capture, where the clearing kernel would only run at replay.
+// resolves it with that device current, clears the counters on `stream` and waits for
+// the clear; it is refused under stream capture, where the clearing kernel would only
+// run at replay.
 int scratch_for_current_device(hipStream_t stream, void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
@@ -3689,6 +3690,9 @@ int scratch_for_current_device(hipStream_t stream, void** out) {
     constexpr int kWords = static_cast<int>(kCounterBytes / sizeof(uint32_t));
     zero_words_kernel<<<dim3((kWords + 255) / 256), dim3(256), 0, stream>>>(static_cast<uint32_t*>(ptr), kWords);
     e = hipGetLastError();
+    // Waited for here, once per device, so that a later call from any stream or
+    // thread runs after the clear, not only one that follows it on `stream`.
+    if (e == hipSuccess) e = hipStreamSynchronize(stream);
     if (e != hipSuccess) {
       set_last_error("fdllm_kv_attn_fwd_noalloc: clearing the scratch failed: %s", hipGetErrorString(e));
       return static_cast<int>(e);

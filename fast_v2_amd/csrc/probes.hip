@@ -16,6 +16,11 @@
 //   fdllm_probe_copy_rows  copies dst[t] = src[idx[t]] for rows of a multiple of 16 bytes
 //                          (at most 16 KB), one wave per row (one row per workgroup),
 //                          every load issued before the first store.
+//   fdllm_probe_mfma       the sustained rate of v_mfma_f32_32x32x16_bf16, the instruction
+//                          of the prefill / full-block kernels: one wave per SIMD, four
+//                          independent accumulator chains per wave (one chain is bound by
+//                          the 48-cycle dependent latency, two or more issue every 32
+//                          cycles), operands in registers, no memory traffic in the loop.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -160,6 +165,32 @@ __global__ __launch_bounds__(64) void probe_copy_rows_kernel(const u32x4* src, i
   }
 }
 
+// rounds x 4 MFMAs per wave on register operands; 256 threads = one wave per SIMD
+__global__ __launch_bounds__(256) void probe_mfma_kernel(float* sink, int rounds, float seed) {
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef float f32x16 __attribute__((ext_vector_type(16)));
+  bf16x8 a, b;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    a[i] = static_cast<__bf16>(seed * static_cast<float>((threadIdx.x + i) & 15));
+    b[i] = static_cast<__bf16>(seed * static_cast<float>((threadIdx.x * 3 + i) & 15));
+  }
+  f32x16 c[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) c[k] = f32x16{};
+#pragma unroll 4
+  for (int n = 0; n < rounds; ++n) {
+#pragma unroll
+    for (int k = 0; k < 4; ++k) c[k] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c[k], 0, 0, 0);
+  }
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) s += c[k][e];
+  if (s == 1234.5f) sink[blockIdx.x * 256 + threadIdx.x] = s;  // keeps the chains live
+}
+
 }  // namespace
 
 extern "C" int fdllm_probe_read_kv(const void* k, const void* v, int64_t k_stride_page, int64_t k_stride_slot,
@@ -213,5 +244,11 @@ extern "C" int fdllm_probe_copy_rows(const void* src, int64_t src_row_bytes, int
   if (nvec <= 64 * 4) probe_copy_rows_kernel<4><<<dim3(rows), dim3(64), 0, s>>>(sp, srv, idx, src_rows, dp, rows, nvec);
   else if (nvec <= 64 * 8) probe_copy_rows_kernel<8><<<dim3(rows), dim3(64), 0, s>>>(sp, srv, idx, src_rows, dp, rows, nvec);
   else probe_copy_rows_kernel<16><<<dim3(rows), dim3(64), 0, s>>>(sp, srv, idx, src_rows, dp, rows, nvec);
+  return hipGetLastError() == hipSuccess ? 0 : FDLLM_PROBE_ERR_LAUNCH;
+}
+
+extern "C" int fdllm_probe_mfma(int workgroups, int rounds, float* sink, void* stream) {
+  if (!sink || workgroups < 1 || workgroups > 65535 || rounds < 1 || rounds > (1 << 24)) return FDLLM_PROBE_ERR_ARGS;
+  probe_mfma_kernel<<<dim3(workgroups), dim3(256), 0, static_cast<hipStream_t>(stream)>>>(sink, rounds, 1.f / 64.f);
   return hipGetLastError() == hipSuccess ? 0 : FDLLM_PROBE_ERR_LAUNCH;
 }

@@ -258,8 +258,10 @@ int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* desc, void* workspace, size_t wo
  *     with <= 8 KV heads, and any full-block decode (<= 256 rows per KV head) of up
  *     to 64 sequences of at most 10240 keys with <= 4 KV heads; calls that need no
  *     workspace (prefill) always fit.
- *   - The first call on a device resolves the scratch and clears its counters on
- *     `stream`; it must not be made under stream capture (FDLLM_ERR_UNSUPPORTED).
+ *   - The first call on a device resolves the scratch, clears its counters on
+ *     `stream` and waits for that clear (so later calls from any stream or thread
+ *     start after it); it must not be made under stream capture
+ *     (FDLLM_ERR_UNSUPPORTED).
  *   - Every call on one device shares that device's scratch, and each call leaves
  *     its counters at zero: calls on one stream run in order, but calls that overlap
  *     in time on one device (other streams, other threads) race. */

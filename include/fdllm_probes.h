@@ -2,7 +2,8 @@
  * libfdllm_probes.so — measurement probes for bench.py (not part of the operator
  * library; no counterpart in the reference): plain data movement in the access pattern
  * and launch shape of the two HBM-bound hot-path calls, the practical floor each call
- * is measured against.
+ * is measured against, and the sustained MFMA rate the MFMA-bound calls are measured
+ * against.
  *
  * Return value: 0, FDLLM_PROBE_ERR_ARGS (nothing launched) or FDLLM_PROBE_ERR_LAUNCH.
  */
@@ -36,6 +37,13 @@ int fdllm_probe_read_kv(const void* k, const void* v, int64_t k_stride_page, int
  * are left unwritten. One wave (workgroup) per row; all loads before the stores. */
 int fdllm_probe_copy_rows(const void* src, int64_t src_row_bytes, int src_rows, const int64_t* idx, void* dst,
                           int rows, int row_bytes, void* stream);
+
+/* Sustained bf16 MFMA rate: `workgroups` workgroups of 256 threads (one wave per SIMD;
+ * one workgroup per compute unit fills the chip), each wave `rounds` rounds of four
+ * independent v_mfma_f32_32x32x16_bf16 chains on register operands (32768 flop each), no
+ * memory traffic. Flops = workgroups * 4 * rounds * 4 * 32768. sink: workgroups * 256
+ * writable floats (written only if the sums hit a fixed constant). */
+int fdllm_probe_mfma(int workgroups, int rounds, float* sink, void* stream);
 
 #ifdef __cplusplus
 }

@@ -62,7 +62,7 @@ def test_probes_library_exports_its_header():
     if not PROBES_LIB.exists():
         pytest.fail(f"{PROBES_LIB} is not built (run __graft_entry__.build())")
     names = _declared_functions([PROBES_HEADER])
-    assert names == {"fdllm_probe_read_kv", "fdllm_probe_copy_rows"}
+    assert names == {"fdllm_probe_read_kv", "fdllm_probe_copy_rows", "fdllm_probe_mfma"}
     out = subprocess.run(["nm", "-D", "--defined-only", str(PROBES_LIB)], capture_output=True, text=True,
                          check=True).stdout
     exported = {line.split()[-1] for line in out.splitlines() if line.strip()}
@@ -73,6 +73,8 @@ def test_probes_library_exports_its_header():
     assert lib.fdllm_probe_copy_rows(None, 16, 1, None, None, 1, 16, None) == -1
     lib.fdllm_probe_read_kv.restype = ctypes.c_int
     assert lib.fdllm_probe_read_kv(*([None] * 2 + [0] * 6 + [None, 0, 32, None, 1, 4, 64, None, None])) == -1
+    lib.fdllm_probe_mfma.restype = ctypes.c_int
+    assert lib.fdllm_probe_mfma(256, 8, None, None) == -1
 
 
 def test_ctypes_table_matches_header():

@@ -25,6 +25,8 @@ def _lib():
     lib.fdllm_probe_read_kv.restype = ctypes.c_int
     lib.fdllm_probe_copy_rows.argtypes = [vp, i64, ctypes.c_int, vp, vp, ctypes.c_int, ctypes.c_int, vp]
     lib.fdllm_probe_copy_rows.restype = ctypes.c_int
+    lib.fdllm_probe_mfma.argtypes = [ctypes.c_int, ctypes.c_int, vp, vp]
+    lib.fdllm_probe_mfma.restype = ctypes.c_int
     return lib
 
 
@@ -86,3 +88,19 @@ def test_probe_rejects_bad_calls(gpu):
     dst = torch.zeros(2, 16384, dtype=torch.bfloat16, device=gpu)
     assert lib.fdllm_probe_copy_rows(src.data_ptr(), 16384 * 2, 4, idx.data_ptr(), dst.data_ptr(), 2, 16384 * 2,
                                      _stream()) == -1
+    # MFMA rate probe: no workgroups, no rounds, no sink
+    out = torch.zeros(256, dtype=torch.float32, device=gpu)
+    assert lib.fdllm_probe_mfma(0, 8, out.data_ptr(), _stream()) == -1
+    assert lib.fdllm_probe_mfma(1, 0, out.data_ptr(), _stream()) == -1
+    assert lib.fdllm_probe_mfma(1, 8, None, _stream()) == -1
+
+
+def test_probe_mfma_runs(gpu):
+    """The MFMA rate probe runs to completion on a full grid (one workgroup per compute
+    unit) and leaves its sink untouched (the sums never hit the sink's constant)."""
+    print("case probe mfma", flush=True)
+    wgs = torch.cuda.get_device_properties(gpu).multi_processor_count
+    sink = torch.zeros(wgs * 256, dtype=torch.float32, device=gpu)
+    assert _lib().fdllm_probe_mfma(wgs, 64, sink.data_ptr(), _stream()) == 0
+    torch.cuda.synchronize()
+    assert int(torch.count_nonzero(sink)) == 0
