@@ -8,7 +8,8 @@ bf16; the 7B-geometry bs16 paged sub-block decode at full size; the contiguous
 static-cache layout vs the paged layout (identical outputs); full 32-token
 blocks (224 rows per KV head); split-KV on/off; causal and block-causal masks;
 block-causal prefill with its KV-cache write; ragged lengths, empty sequences,
-a single visible key; fp16; head_dim 64.
+a single visible key; fp16; head_dim 64; NaN in every row no query may see (past
+the lengths, unreferenced pages) leaving every kernel family's output unchanged.
 """
 from pathlib import Path
 
@@ -801,3 +802,79 @@ def test_large_batch_grid(gpu, B, paged):
     sel = torch.cat([torch.arange(3), torch.randperm(B - 3, generator=g)[:397] + 3])
     exp = oa.attention_np(q[sel].float(), k[sel].float(), v[sel].float(), seqlens[sel])
     _check(out[sel], exp)
+
+
+def _poison_paged(pool: torch.Tensor, page_table: torch.Tensor, seqlens: torch.Tensor, page_size: int,
+                  extra_pages: int, fill: float) -> torch.Tensor:
+    """The pool with `extra_pages` unreferenced pages appended and every (page, slot) that
+    no sequence sees (past its length, or on a page no table entry names) set to `fill`."""
+    P = pool.shape[0]
+    out = torch.cat([pool, torch.zeros((extra_pages,) + tuple(pool.shape[1:]), dtype=pool.dtype)])
+    seen = torch.zeros(P + extra_pages, page_size, dtype=torch.bool)
+    for b in range(page_table.shape[0]):
+        n = int(seqlens[b])
+        for j in range(0, n, page_size):
+            seen[int(page_table[b, j // page_size]), : min(page_size, n - j)] = True
+    out[~seen] = fill
+    return out
+
+
+@pytest.mark.parametrize("case", ["paged_subblock", "paged_full_block", "static_split", "static_general",
+                                  "block_causal_prefill", "fp32"])
+def test_unread_rows_poisoned_with_nan(gpu, case):
+    """Keys past each sequence's visible length have no influence (the invariant the reference's
+    SDPA shim states with its -inf mask, tests/test_focus.py:220-224): every K/V row that no
+    query may see (slots past the length, unreferenced pages, static-cache rows past the
+    length) is set to NaN, and the output must be bit for bit the output with zeros there,
+    on every kernel family the dispatcher picks (split decode, full-block ring split, static
+    cache split and general kernels, block-causal prefill ring, fp32)."""
+    print(f"case poisoned rows {case}", flush=True)
+    nan = float("nan")
+    if case.startswith("paged"):
+        wl = workloads.kv_decode_paged(seed=41, batch=16, active=8 if case == "paged_subblock" else 32)
+        sl = wl.seqlens.clone()
+        sl[::3] -= 7  # partial last pages
+        outs = []
+        for fill in (0.0, nan):
+            kp = _poison_paged(wl.k_pool, wl.page_table, sl, wl.page_size, 3, fill)
+            vp = _poison_paged(wl.v_pool, wl.page_table, sl, wl.page_size, 3, fill)
+            outs.append(ops.block_attn(wl.q.to(gpu), kp.to(gpu), vp.to(gpu), sl.to(gpu), wl.scale,
+                                       page_table=wl.page_table.to(gpu), page_size=wl.page_size).cpu())
+        exp = oa.attention_np(wl.q.float(), wl.k_pool.float(), wl.v_pool.float(), sl, wl.scale,
+                              page_table=wl.page_table, page_size=wl.page_size)
+    else:
+        g = torch.Generator().manual_seed(43)
+        dt = torch.float32 if case == "fp32" else torch.bfloat16
+        if case == "block_causal_prefill":
+            B, Sq, Hq, Hkv, S = 2, 512, 28, 4, 640
+            sl = torch.tensor([512, 576], dtype=torch.int32)  # queries at positions sl - 512 ..
+        elif case == "fp32":
+            B, Sq, Hq, Hkv, S = 1, 32, 12, 2, 600
+            sl = torch.tensor([544], dtype=torch.int32)
+        else:
+            B, Sq, Hq, Hkv, S = 6, 8, 28, 4, 1500
+            sl = torch.tensor([1, 31, 33, 700, 1029, 1400], dtype=torch.int32)
+        q = torch.randn(B, Sq, Hq, 128, generator=g).to(dt)
+        k = torch.randn(B, S, Hkv, 128, generator=g).to(dt)
+        v = torch.randn(B, S, Hkv, 128, generator=g).to(dt)
+        kw = {}
+        if case == "block_causal_prefill":
+            kw = dict(mask_mode=_ffi.MASK_BLOCK_CAUSAL, mask_block=32)
+        elif case == "static_general":
+            kw = dict(decode_kernel=False, kv_split=64)
+        outs = []
+        for fill in (0.0, nan):
+            kc, vc = k.clone(), v.clone()
+            for b in range(B):
+                kc[b, int(sl[b]):] = fill
+                vc[b, int(sl[b]):] = fill
+            outs.append(ops.block_attn(q.to(gpu), kc.to(gpu), vc.to(gpu), sl.to(gpu), **kw).cpu())
+        if case == "block_causal_prefill":
+            exp = None  # the block-causal kernel's values are checked elsewhere; here only the invariant
+        else:
+            exp = oa.attention_np(q.float(), k.float(), v.float(), sl)
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[1]).all(), "NaN from an unread row reached the output"
+    assert torch.equal(outs[0], outs[1]), "rows past the visible lengths changed the output"
+    if exp is not None:
+        _check(outs[0], exp)
