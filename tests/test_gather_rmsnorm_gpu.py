@@ -382,3 +382,29 @@ def test_gather_and_scatter_large_batch(gpu, H):
     ops.scatter_rows(vals.to(gpu), sidx.to(gpu), c_gpu)
     exp_c = cache.clone().scatter_(1, sidx.unsqueeze(-1).expand(-1, -1, H), vals)
     assert torch.equal(c_gpu.cpu(), exp_c)
+
+
+@pytest.mark.parametrize("H,dtype", [(3584, torch.bfloat16), (128, torch.bfloat16), (4096, torch.float16),
+                                     (2056, torch.bfloat16), (512, torch.float32)])
+def test_unselected_rows_poisoned_with_nan(gpu, H, dtype):
+    """Only the selected rows are read: NaN in every row no index names leaves the normed
+    rows and the gathered copy bit for bit as with zeros there, on every width class (the
+    register-vector kernels and the element loop) and for fp32 hidden states."""
+    print(f"case poisoned gather H={H} {dtype}", flush=True)
+    g = torch.Generator().manual_seed(H)
+    B, S, T = 2, 300, 77
+    hidden = torch.randn(B, S, H, generator=g).to(dtype)
+    idx = torch.stack([torch.randperm(S, generator=g)[:T] for _ in range(B)])
+    w = (1 + 0.02 * torch.randn(H, generator=g)).to(dtype)
+    outs = []
+    for fill in (0.0, float("nan")):
+        h = hidden.clone()
+        keep = torch.zeros(B, S, dtype=torch.bool)
+        keep[torch.arange(B)[:, None], idx] = True
+        h[~keep] = fill
+        normed, gathered = ops.gather_rmsnorm(h.to(gpu), idx.to(gpu), w.to(gpu), 1e-6)
+        outs.append((normed.cpu(), gathered.cpu()))
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[1][0]).all() and torch.isfinite(outs[1][1]).all()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert torch.equal(outs[1][1], hidden[torch.arange(B)[:, None], idx])
