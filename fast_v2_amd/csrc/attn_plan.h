@@ -27,6 +27,18 @@ constexpr int kDecodeMaxTiles = 160;   // 32-key tiles per split: page ids stage
 constexpr int kBalMaxPages = 4096;     // page-table entries the cross-sequence decode kernel stages
 constexpr int kPrefillWaves = 8;       // waves (x 32 query rows) per prefill workgroup
 constexpr int kSplitTargetWG = 256;    // MI355X compute units
+// Teams of 4 waves per split decode workgroup: two (512 threads, one workgroup per compute
+// unit; the default) or one (256 threads, two workgroups per compute unit and twice the
+// slots). One team was measured slower on the bs16 7B sub-block step, 31.4 against
+// 25.5 us: no split is longer than the median any more, but the loop is bound by HBM and
+// ends no earlier, and folding a unit's 8 splits in one 256-thread workgroup takes 6.8
+// against 2.4 us.
+#ifndef FDLLM_DECODE_TEAMS
+#define FDLLM_DECODE_TEAMS 2
+#endif
+constexpr int kDecodeTeams = FDLLM_DECODE_TEAMS;
+static_assert(kDecodeTeams == 1 || kDecodeTeams == 2, "one or two teams per split decode workgroup");
+constexpr int kDecodeSlotsTarget = kSplitTargetWG * (kDecodeTeams == 1 ? 2 : 1);
 constexpr int kSplitMaxChunk = kDecodeMaxTiles * 32;  // keys per split: page ids staged in LDS
 constexpr int kBalancedMaxBatch = 64;  // one wave lane per sequence in the partition search
 constexpr size_t kCounterBytes = 64 * 1024;  // arrival counters at the head of the workspace
@@ -159,7 +171,7 @@ inline int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
       }
       if (d->kv_split == 0 && B <= kBalancedMaxBatch) {
         pl->chunk = 0;
-        slots = std::max<int64_t>((kSplitTargetWG + hkv - 1) / hkv, B * min_splits);
+        slots = std::max<int64_t>((kDecodeSlotsTarget + hkv - 1) / hkv, B * min_splits);
         pl->n_splits = static_cast<int>(slots);
         split_possible = slots > B;
       } else {

@@ -1037,10 +1037,11 @@ __device__ __forceinline__ void merge_splits_n(const AttnParams& p, int b, int k
 //     with one atomic; the last workgroup of the unit merges all partials
 //     (merge_splits) and resets the counter, so no second kernel is launched.
 template <int NS, bool F16, bool PAGED>
-__global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARAMS, const AttnParams p) {
+__global__ __launch_bounds__(256 * kDecodeTeams, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARAMS, const AttnParams p) {
   FDLLM_LEAD_LOCAL;
   FDLLM_STAMP(0, __builtin_amdgcn_s_memrealtime());  // start
   constexpr int D = 128;
+  constexpr int NT = 256 * kDecodeTeams;  // threads
   constexpr int KT = 32;
   constexpr int KS = D + 8;
   constexpr int VS = D + 16;
@@ -1049,7 +1050,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   constexpr int KBUF = KT * KS;
   constexpr int VBUF = KT * VS;
   // [team][buffer] K then V tiles; reused for the team merge at the end
-  __shared__ __attribute__((aligned(16))) uint16_t sKV[2][2][KBUF + VBUF];
+  __shared__ __attribute__((aligned(16))) uint16_t sKV[kDecodeTeams][2][KBUF + VBUF];
   __shared__ int sPage[kMaxPages];
   // the whole page table when it is small: read together with the lengths, so the
   // page ids of the workgroup's range need no second round trip after the partition
@@ -1061,7 +1062,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   const int wave = tid >> 6;
   // wave-uniform by construction; readfirstlane lets the compiler keep the
   // per-team buffer descriptors in scalar registers
-  const int team = __builtin_amdgcn_readfirstlane(wave >> 2);
+  const int team = kDecodeTeams == 2 ? __builtin_amdgcn_readfirstlane(wave >> 2) : 0;
   const int wt = wave & 3;
   const int ttid = tid & 255;  // thread index within the team
   const int l16 = lane & 15;
@@ -1070,11 +1071,11 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   const int kvh = blockIdx.y;
   const int n_pt = PAGED ? ld.B * ld.max_pages : 0;
   const bool pt_prefetch = PAGED && n_pt <= kPrefetchPages;  // uniform
-  int pf[kPrefetchPages / 512];
+  int pf[kPrefetchPages / NT];
   if (pt_prefetch) {
 #pragma unroll
-    for (int u = 0; u < kPrefetchPages / 512; ++u) {
-      const int idx = tid + 512 * u;
+    for (int u = 0; u < kPrefetchPages / NT; ++u) {
+      const int idx = tid + NT * u;
       pf[u] = idx < n_pt ? ld.page_table[idx] : 0;
     }
   }
@@ -1092,7 +1093,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   si.kv_end = dp.kv_end;
   // at most kMaxPages tiles by construction of the partition (the min keeps LDS indexing in bounds)
   const int ntiles = min(kMaxPages, k_hi > k_lo ? (k_hi - k_lo + KT - 1) / KT : 0);
-  const int nsteps = (ntiles + 1) / 2;  // tiles per team, rounded up (both teams run every step)
+  const int nsteps = (ntiles + kDecodeTeams - 1) / kDecodeTeams;  // tiles per team, rounded up (every team runs every step)
 
   // ---- query fragments and row limits of this wave's 16 rows
   u32x4 qf[4];
@@ -1114,13 +1115,13 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   if constexpr (PAGED) {
     if (pt_prefetch) {
 #pragma unroll
-      for (int u = 0; u < kPrefetchPages / 512; ++u) {
-        const int idx = tid + 512 * u;
+      for (int u = 0; u < kPrefetchPages / NT; ++u) {
+        const int idx = tid + NT * u;
         if (idx < n_pt) sAllPages[idx] = pf[u];
       }
     } else {
       const int32_t* pt_row = ld.page_table + static_cast<int64_t>(b) * ld.max_pages;
-      for (int i = tid; i < ntiles; i += 512) sPage[i] = pt_row[(k_lo + i * KT) >> p.page_shift];
+      for (int i = tid; i < ntiles; i += NT) sPage[i] = pt_row[(k_lo + i * KT) >> p.page_shift];
     }
   }
 
@@ -1151,9 +1152,9 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
 
   if constexpr (PAGED) __syncthreads();  // sPage visible
 
-  // tile j of this team = tile 2j + team of the range
+  // tile j of this team = tile kDecodeTeams j + team of the range
   auto load_tile = [&](Stage& sg, int j) {
-    const int t = 2 * j + team;
+    const int t = kDecodeTeams * j + team;
     const int kb = k_lo + t * KT;
     const int valid = __builtin_amdgcn_readfirstlane(max(0, min(KT, k_hi - kb)));
     int64_t koffs, voffs;
@@ -1258,7 +1259,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
     lds_barrier();
     if (FDLLM_TIMELINE && j == 0) FDLLM_STAMP(2, __builtin_amdgcn_s_memrealtime());  // first tiles in LDS
     load_tile(sg, j + NS);
-    const int t = 2 * j + team;
+    const int t = kDecodeTeams * j + team;
     if (t < ntiles) compute_tile(j & 1, k_lo + t * KT);  // wave-uniform
   };
   if (nsteps > 0) {
@@ -1278,6 +1279,9 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   // ---- merge the two teams: team 1 hands (m, l, O) to team 0 through LDS
   float* xfer = reinterpret_cast<float*>(&sKV[0][0][0]);  // [4 waves][64 lanes][NDT * 4 + 2]
   constexpr int XS = NDT * 4 + 2;
+  if constexpr (kDecodeTeams == 1) {
+    l_run = group4_allreduce_sum(l_run);
+  } else {
   lds_barrier();  // every wave is done with the tiles
   if (team == 1) {
     float* x = xfer + (wt * 64 + lane) * XS;
@@ -1303,6 +1307,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
       for (int j = 0; j < 4; ++j) acc[dt][j] = acc[dt][j] * a0 + x[dt * 4 + j] * a1;
     m_run = m_new;
     l_run = group4_allreduce_sum(l_run);
+  }
   }
 
   // ---- epilogue (team 0 holds the workgroup's result): rows r = 16 wt + l16,
@@ -1350,7 +1355,7 @@ __global__ __launch_bounds__(512, 2) void kv_split_decode_kernel(FDLLM_LEAD_PARA
   __syncthreads();
   FDLLM_STAMP(4, __builtin_amdgcn_s_memrealtime());  // partial stored, arrival counted
   if (!s_last) return;
-  merge_splits_n<F16>(p, b, kvh, slot0, n_act, tid, 512);
+  merge_splits_n<F16>(p, b, kvh, slot0, n_act, tid, NT);
   if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
   FDLLM_STAMP(5, __builtin_amdgcn_s_memrealtime());  // merge written (last arrival)
 }
@@ -3586,11 +3591,11 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
     const bool paged = p.page_table != nullptr;
     const dim3 grid = to_dim3(ls.main_grid);
     if (f16) {
-      if (paged) kv_split_decode_kernel<kDecodeStages, true, true><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
-      else kv_split_decode_kernel<kDecodeStages, true, false><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+      if (paged) kv_split_decode_kernel<kDecodeStages, true, true><<<grid, dim3(256 * kDecodeTeams), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+      else kv_split_decode_kernel<kDecodeStages, true, false><<<grid, dim3(256 * kDecodeTeams), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
     } else {
-      if (paged) kv_split_decode_kernel<kDecodeStages, false, true><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
-      else kv_split_decode_kernel<kDecodeStages, false, false><<<grid, dim3(512), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+      if (paged) kv_split_decode_kernel<kDecodeStages, false, true><<<grid, dim3(256 * kDecodeTeams), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
+      else kv_split_decode_kernel<kDecodeStages, false, false><<<grid, dim3(256 * kDecodeTeams), 0, s>>>(FDLLM_LEAD_ARGS(p), p);
     }
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }
