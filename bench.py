@@ -330,7 +330,7 @@ def bench_decode_full(torch, args):
     return res
 
 
-def cpu_baseline_decode(torch, wl):
+def cpu_baseline_decode(torch, wl, warmup: int = 10, measured: int = 50, what: str = "the full bs16 batch"):
     """Reference CPU path (SDPA shim) on the same bs16 inputs, bf16, contiguous static cache."""
     from oracle import attention as oa
 
@@ -346,9 +346,9 @@ def cpu_baseline_decode(torch, wl):
         pages = wl.page_table[b, pos // wl.page_size].long()
         k[b, :L] = layer_k[pages, pos % wl.page_size]
         v[b, :L] = layer_v[pages, pos % wl.page_size]
-    st = _cpu_protocol(torch, lambda: oa.sdpa_kvcache(wl.q, k, v, wl.seqlens, scaling=wl.scale))
+    st = _cpu_protocol(torch, lambda: oa.sdpa_kvcache(wl.q, k, v, wl.seqlens, scaling=wl.scale), warmup, measured)
     return _cpu_result(st, "us/step", f"SDPA shim (tests/test_focus.py:205-228 restated in oracle/attention.py), "
-                       f"bf16, the full bs16 batch of one layer, contiguous [16, {max_s}, 4, 128] cache")
+                       f"bf16, {what} of one layer, contiguous [16, {max_s}, 4, 128] cache")
 
 
 # ---------------------------------------------------------------------------
@@ -957,6 +957,12 @@ def main() -> int:
         _log("cpu baseline (small fp32 decode, SDPA shim) ...")
         extra["small_fp32_cpu"] = cpu_baseline_small_fp32(torch)
     if not args.no_cpu_baseline:
+        if "block_decode_full" in extra:
+            _log("cpu baseline (bs16 full-block step) ...")
+            from fast_v2_amd import workloads as _wls
+            extra["block_decode_full"]["cpu_baseline"] = cpu_baseline_decode(
+                torch, _wls.kv_decode_paged(seed=0, active=32), warmup=3, measured=15,
+                what="the full bs16 batch with all 32 block queries")
         if "gather_rmsnorm" in extra:
             _log("cpu baseline (gather + RMSNorm) ...")
             extra["gather_rmsnorm"]["cpu_baseline"] = cpu_baseline_gather(torch)
