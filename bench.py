@@ -704,26 +704,33 @@ def calibrate_copies(torch):
     torch.cuda.empty_cache()
     # the decode step's read pattern at a size where its fixed phases no longer count:
     # fdllm_probe_read_kv over a contiguous [64, 4096, 4, 128] bf16 cache (537 MB of K and
-    # V), the keys dealt over 64 / 128 / 256 slots per KV head (1 / 2 / 4 workgroups of
-    # 512 threads per compute unit)
+    # V), stored head-major (one KV head's keys one contiguous run, as the head-major pages
+    # of the headline step) or token-major (a head's key rows 256 B at a 1 KB stride), the
+    # keys dealt over 64 / 128 / 256 slots per KV head (1 / 2 / 4 workgroups of 512
+    # threads per compute unit)
     probes = _probes()
     B, S, H, D = 64, 4096, 4, 128
-    k = torch.randn(B, S, H, D, device="cuda").to(torch.bfloat16)
-    v = torch.randn_like(k)
     sl = torch.full((B,), S, dtype=torch.int32, device="cuda")
     sink = torch.zeros(4, dtype=torch.int32, device="cuda")
-    ks, vs = k.stride(), v.stride()
     n = B * S * H * D * 2 * 2
-    for slots in (64, 128, 256):
-        def step(i, slots=slots):
-            rc = probes.fdllm_probe_read_kv(k.data_ptr(), v.data_ptr(), ks[0], ks[1], ks[2], vs[0], vs[1], vs[2],
-                                            None, 0, 0, sl.data_ptr(), B, H, slots, sink.data_ptr(),
-                                            _stream_ptr(torch))
-            if rc != 0:
-                raise RuntimeError(f"fdllm_probe_read_kv failed ({rc})")
-        us = _time_graph(torch, step, 20, 4)
-        res[f"read_kv_537MB_{slots}_slots"] = {"us": round(us, 2), "GBs_read": round(n / (us * 1e-6) / 1e9, 1)}
-    del k, v
+    for layout in ("head_major", "token_major"):
+        if layout == "head_major":
+            k = torch.randn(B, H, S, D, device="cuda").to(torch.bfloat16).transpose(1, 2)
+        else:
+            k = torch.randn(B, S, H, D, device="cuda").to(torch.bfloat16)
+        v = torch.randn_like(k)  # the same strides as k
+        ks, vs = k.stride(), v.stride()
+        for slots in (64, 128, 256):
+            def step(i, slots=slots, k=k, v=v, ks=ks, vs=vs):
+                rc = probes.fdllm_probe_read_kv(k.data_ptr(), v.data_ptr(), ks[0], ks[1], ks[2], vs[0], vs[1],
+                                                vs[2], None, 0, 0, sl.data_ptr(), B, H, slots, sink.data_ptr(),
+                                                _stream_ptr(torch))
+                if rc != 0:
+                    raise RuntimeError(f"fdllm_probe_read_kv failed ({rc})")
+            us = _time_graph(torch, step, 20, 4)
+            res[f"read_kv_537MB_{layout}_{slots}_slots"] = {"us": round(us, 2),
+                                                            "GBs_read": round(n / (us * 1e-6) / 1e9, 1)}
+        del k, v
     torch.cuda.empty_cache()
     return res
 
