@@ -253,7 +253,7 @@ int fdllm_kv_attn_fwd(const fdllm_kv_attn_desc* desc, void* workspace, size_t wo
  * hipMalloc). It calls no hipMalloc / hipFree.
  *   - A call whose fdllm_kv_attn_workspace_size exceeds FDLLM_KV_ATTN_SCRATCH_BYTES
  *     is rejected with FDLLM_ERR_WORKSPACE (nothing launched). At head_dim 128 with
- *     the automatic split (kv_split 0) the scratch holds any sub-block decode
+ *     the automatic split (kv_split 0), in the default build, the scratch holds any sub-block decode
  *     (<= 64 query rows per KV head) of up to 64 sequences of at most 5120 keys
  *     with <= 8 KV heads, and any full-block decode (<= 256 rows per KV head) of up
  *     to 64 sequences of at most 10240 keys with <= 4 KV heads; calls that need no
