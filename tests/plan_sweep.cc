@@ -92,7 +92,7 @@ static void check_plan(const fdllm_kv_attn_desc& d, const Plan& pl) {
       i128 slots;
       if (pl.chunk == 0) {
         CHECK(Bm <= kBalancedMaxBatch, "per-sequence partition batch: %s", describe(d));
-        CHECK(pl.n_splits >= Bm * cdiv(max_t, kDecodeMaxTiles) && pl.n_splits >= cdiv(kSplitTargetWG, hkv),
+        CHECK(pl.n_splits >= Bm * cdiv(max_t, kDecodeMaxTiles) && pl.n_splits >= cdiv(kDecodeSlotsTarget, hkv),
               "slots %d: %s", pl.n_splits, describe(d));
         slots = pl.n_splits;
       } else {

@@ -17,10 +17,13 @@ ROOT = Path(__file__).resolve().parent.parent
 
 
 @pytest.mark.skipif(shutil.which("g++") is None, reason="needs g++")
-def test_planner_sweep_under_asan_ubsan(tmp_path):
+@pytest.mark.parametrize("defines", [[], ["-DFDLLM_DECODE_TEAMS=1"]], ids=["default", "decode_one_team"])
+def test_planner_sweep_under_asan_ubsan(tmp_path, defines):
+    """Swept for the default build and for the build option of one team per split decode
+    workgroup (twice the slots per KV head)."""
     exe = tmp_path / "plan_sweep"
     cmd = ["g++", "-std=c++17", "-O1", "-g", "-fno-omit-frame-pointer",
-           "-fsanitize=address,undefined", "-fno-sanitize-recover=all",
+           "-fsanitize=address,undefined", "-fno-sanitize-recover=all", *defines,
            "-I", str(ROOT / "include"), "-I", str(ROOT / "fast_v2_amd" / "csrc"),
            str(ROOT / "tests" / "plan_sweep.cc"), "-o", str(exe)]
     subprocess.run(cmd, check=True, capture_output=True, text=True, timeout=300)
