@@ -41,6 +41,11 @@ static_assert(kDecodeTeams == 1 || kDecodeTeams == 2, "one or two teams per spli
 constexpr int kDecodeSlotsTarget = kSplitTargetWG * (kDecodeTeams == 1 ? 2 : 1);
 constexpr int kSplitMaxChunk = kDecodeMaxTiles * 32;  // keys per split: page ids staged in LDS
 constexpr int kBalancedMaxBatch = 64;  // one wave lane per sequence in the partition search
+// fp32 kernel: key splits up to about two workgroups per CU. On a batch-1, 12 / 2-head block
+// of 32 queries over 544 keys (96 row blocks): 3 splits 16.4 us, 5 (this target) 13.8 us,
+// 9 splits 15.5 us, no split 27.4 us.
+constexpr int kF32TargetWG = 512;
+constexpr int kF32MaxSplits = 16;      // fp32 kernel: key splits per row block at most
 constexpr size_t kCounterBytes = 64 * 1024;  // arrival counters at the head of the workspace
 constexpr uint32_t kMaxGridX = 0x7fffffffu;  // grid limits of a launch
 constexpr uint32_t kMaxGridYZ = 65535u;
@@ -101,7 +106,9 @@ inline int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
                   "fdllm_kv_attn: batch x num_kv_heads = %lld above %u",
                   static_cast<long long>(d->batch) * d->num_kv_heads, kMaxGridYZ);
   if (d->dtype == FDLLM_DTYPE_F32) {
-    // fp32: kv_attn_f32_kernel, no workspace, no key split; pages of any power of two
+    // fp32: kv_attn_f32_kernel; pages of any power of two. Keys are split (chunk keys
+    // per split, a multiple of the kernel's 64-key chunk) when the row blocks alone give
+    // fewer than kF32TargetWG workgroups; kv_attn_combine_kernel then folds the partials.
     FDLLM_CHECK_ARG(d->page_table == nullptr ||
                         (d->page_size > 0 && (d->page_size & (d->page_size - 1)) == 0 && d->max_pages > 0),
                     "fdllm_kv_attn: page table needs a power-of-two page_size and max_pages > 0");
@@ -113,11 +120,31 @@ inline int make_plan(const fdllm_kv_attn_desc* d, Plan* pl) {
     pl->decode = false;
     pl->MT = 0;
     pl->rows_per_wg = 4 * FDLLM_F32_ROWS_PER_WAVE;
-    pl->n_rb = 1;
-    pl->n_splits = 1;
-    pl->chunk = 0;
     pl->R = static_cast<int>(rows);
-    pl->ws_o_bytes = pl->ws_ml_bytes = 0;
+    pl->n_rb = static_cast<int>((rows + pl->rows_per_wg - 1) / pl->rows_per_wg);
+    const int64_t chunks = std::max<int64_t>(1, (plan_max_keys(d) + 63) / 64);  // 64-key chunks of the longest
+    const int64_t units = static_cast<int64_t>(d->batch) * d->num_kv_heads * pl->n_rb;
+    int64_t per;  // chunks per split
+    if (d->kv_split > 0) {
+      per = (static_cast<int64_t>(d->kv_split) + 63) / 64;
+    } else if (units >= kF32TargetWG || units == 0) {  // units == 0: an empty call (nothing launches)
+      per = chunks;
+    } else {
+      const int64_t splits = (kF32TargetWG + units - 1) / std::max<int64_t>(units, 1);
+      per = (chunks + splits - 1) / splits;
+    }
+    per = std::max<int64_t>(per, (chunks + kF32MaxSplits - 1) / kF32MaxSplits);  // at most kF32MaxSplits splits
+    per = std::max<int64_t>(1, std::min(per, chunks));
+    pl->chunk = static_cast<int>(per * 64);
+    pl->n_splits = static_cast<int>((chunks + per - 1) / per);
+    if (pl->n_splits > 1) {
+      FDLLM_CHECK_ARG(units * pl->n_splits * pl->rows_per_wg < (int64_t{1} << 31) / 128,
+                      "fdllm_kv_attn: too many fp32 split slots");
+      pl->ws_o_bytes = static_cast<size_t>(units) * pl->n_splits * pl->rows_per_wg * d->head_dim * sizeof(float);
+      pl->ws_ml_bytes = static_cast<size_t>(units) * pl->n_splits * pl->rows_per_wg * 2 * sizeof(float);
+    } else {
+      pl->ws_o_bytes = pl->ws_ml_bytes = 0;
+    }
     return FDLLM_OK;
   }
   // Each thread stages aligned groups of 2048 / head_dim keys from one page.
@@ -380,10 +407,21 @@ inline int plan_launches(const fdllm_kv_attn_desc* d, const Plan& pl, LaunchSet*
   ls->second_grid = GridDims{1, 1, 1};
   switch (pl.kind) {
     case kPlanF32: {
-      const int64_t rwg = 4 * FDLLM_F32_ROWS_PER_WAVE;
-      ls->main_grid = GridDims{static_cast<uint32_t>((pl.R + rwg - 1) / rwg), static_cast<uint32_t>(hkv),
-                               static_cast<uint32_t>(B)};
+      // x = row block + n_rb * split
+      ls->main_grid = GridDims{static_cast<uint32_t>(static_cast<int64_t>(pl.n_rb) * pl.n_splits),
+                               static_cast<uint32_t>(hkv), static_cast<uint32_t>(B)};
       ls->main_block = 256;
+      if (pl.n_splits > 1) {
+        // combine: one workgroup row per (sequence, KV head, row block)
+        const int rpb = 256 / (d->head_dim / 8);
+        const int64_t units = static_cast<int64_t>(B) * hkv * pl.n_rb;
+        FDLLM_CHECK_ARG(units <= static_cast<int64_t>(kMaxGridYZ),
+                        "fdllm_kv_attn_fwd: %lld split units exceed the merge grid; pass a larger kv_split",
+                        static_cast<long long>(units));
+        ls->second = true;
+        ls->second_grid = GridDims{static_cast<uint32_t>((pl.rows_per_wg + rpb - 1) / rpb),
+                                   static_cast<uint32_t>(units), 1};
+      }
       break;
     }
     case kPlanBalancedDecode:

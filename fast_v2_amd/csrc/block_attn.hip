@@ -1878,12 +1878,17 @@ __device__ __forceinline__ float halves_sum(float v) {
 // base 2 (scores pre-multiplied by scale * log2 e), rescaled whenever the chunk maximum
 // moves it. The workgroup runs to the largest key bound of its rows; each row masks the
 // keys past its own.
-// query rows per wave of kv_attn_f32_kernel: on the 12 / 2-head block of 32 queries over
-// 544 keys, 1: 27.8 us, 2: 36.2 us, 4: 72.9 us (fewer rows per workgroup, more workgroups
-// in flight; the previous one-wave-per-row form without staging: 85 us). The PV products
-// run over every key of a chunk, unrolled, instead of a loop to the chunk's last visible
-// key: 27.8 -> 26.9 us, the same sums bit for bit; the query row held in registers instead
-// of broadcast reads from LDS was slower (36.1 us).
+// Key splits: a row block's keys are cut into splits of p.chunk keys (a multiple of the
+// 64-key chunk) over x = row block + n_rb * split; a row block whose keys fit one split
+// writes its rows directly, otherwise each split writes unnormalised (O, m, l) partials
+// (m in base-2 score units) that kv_attn_combine_kernel<..., true> folds. On the 12 / 2-head
+// block of 32 queries over 544 keys: 27.4 us unsplit, 13.8 us in 5 splits.
+// query rows per wave of kv_attn_f32_kernel, unsplit: 1: 27.8 us, 2: 36.2 us, 4: 72.9 us
+// (fewer rows per workgroup, more workgroups in flight; the previous one-wave-per-row form
+// without staging: 85 us). The PV products run over every key of a chunk, unrolled,
+// instead of a loop to the chunk's last visible key: 27.8 -> 26.9 us, the same sums bit for
+// bit; the query row held in registers instead of broadcast reads from LDS was slower
+// (36.1 us).
 // (FDLLM_F32_ROWS_PER_WAVE, the rows per wave, is set in attn_plan.h: the plan sizes the
 // grid from it.)
 template <int DPL, bool PAGED>
@@ -1904,7 +1909,10 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
   const int b = blockIdx.z;
   const int kvh = blockIdx.y;
   const int R = p.Sq * p.G;
-  const int r0 = static_cast<int>(blockIdx.x) * RWG;
+  // x = row block + n_rb * split
+  const int split = static_cast<int>(blockIdx.x) / p.n_rb;
+  const int rb = static_cast<int>(blockIdx.x) - split * p.n_rb;
+  const int r0 = rb * RWG;
   int seqlen = p.seqlens[b];
   if (seqlen > p.max_seqlen) seqlen = p.max_seqlen;
   if (PAGED && seqlen > p.max_pages * p.page_size) seqlen = p.max_pages * p.page_size;
@@ -1912,6 +1920,12 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
   const int qs = p.q_start ? p.q_start[b] : seqlen - p.Sq;
   // key bounds never decrease with the query token, so the workgroup's last row has the largest
   const int kv_end = __builtin_amdgcn_readfirstlane(row_key_limit(p, seqlen, qs, (min(r0 + RWG, R) - 1) / p.G));
+  // this workgroup's keys: split `split` of p.chunk keys (the row block's splits with keys;
+  // a row block without keys still has split 0, which writes its zero rows)
+  const int n_act = max(1, (kv_end + p.chunk - 1) / p.chunk);
+  if (split >= n_act) return;  // uniform
+  const int k_lo = split * p.chunk;  // < kv_end, or 0
+  const int k_hi = static_cast<int>(min<int64_t>(kv_end, static_cast<int64_t>(k_lo) + p.chunk));
 
   int lim[RW], tq[RW], hq[RW];
   bool live[RW];
@@ -1922,7 +1936,7 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
     const int rc = live[i] ? r : R - 1;
     tq[i] = rc / p.G;
     hq[i] = kvh * p.G + (rc - tq[i] * p.G);
-    lim[i] = __builtin_amdgcn_readfirstlane(row_key_limit(p, seqlen, qs, tq[i]));
+    lim[i] = __builtin_amdgcn_readfirstlane(min(row_key_limit(p, seqlen, qs, tq[i]), k_hi));
     const float* q = reinterpret_cast<const float*>(p.q) + b * p.q_sb + tq[i] * p.q_ss + hq[i] * p.q_sh;
     for (int d = lane; d < D; d += 64) sQ[w * RW + i][d] = q[d];
   }
@@ -1938,7 +1952,7 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
     }
   };
   // load e of a thread: f32x4 index tid + 256 e of the chunk = key idx / (D / 4), column
-  // 4 (idx % (D / 4)); keys at or past kv_end read as zero
+  // 4 (idx % (D / 4)); keys at or past k_hi read as zero
   f32x4 kr[PER], vr[PER];
   auto load_chunk = [&](int k0) {
 #pragma unroll
@@ -1946,7 +1960,7 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
       const int idx = tid + 256 * e;
       const int key = k0 + idx / (D / 4);
       const int c = 4 * (idx % (D / 4));
-      if (key < kv_end) {
+      if (key < k_hi) {
         kr[e] = *reinterpret_cast<const f32x4*>(kb + row_off(key, true) + c);
         vr[e] = *reinterpret_cast<const f32x4*>(vb + row_off(key, false) + c);
       } else {
@@ -1963,8 +1977,8 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
 #pragma unroll
     for (int j = 0; j < DPL; ++j) o[i][j] = 0.f;
   }
-  if (kv_end > 0) load_chunk(0);
-  for (int k0 = 0; k0 < kv_end; k0 += CK) {
+  if (k_hi > k_lo) load_chunk(k_lo);
+  for (int k0 = k_lo; k0 < k_hi; k0 += CK) {
     __syncthreads();  // every wave is done with the previous chunk (and sQ is written)
 #pragma unroll
     for (int e = 0; e < PER; ++e) {
@@ -1975,7 +1989,7 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
       *reinterpret_cast<f32x4*>(&sV[key * D + c]) = vr[e];
     }
     __syncthreads();
-    if (k0 + CK < kv_end) load_chunk(k0 + CK);  // in flight during this chunk's math
+    if (k0 + CK < k_hi) load_chunk(k0 + CK);  // in flight during this chunk's math
     const int key = k0 + lane;
     // four partial sums per row (independent FMA chains), added at the end
     float acc[RW][4];
@@ -2006,8 +2020,8 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
       for (int j = 0; j < DPL; ++j) o[i][j] *= alpha;
       m[i] = m_new;
     }
-    // every key of the chunk in order, unrolled: keys past kv_end hold p = 0 and V rows
-    // of zeros (never loaded), so they add exactly nothing
+    // every key of the chunk in order, unrolled: keys past k_hi hold p = 0 and V rows of
+    // zeros (never loaded), so they add exactly nothing
 #pragma unroll
     for (int kk = 0; kk < CK; kk += 4) {
       f32x4 pp[RW];
@@ -2024,6 +2038,21 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
           for (int j = 0; j < DPL; ++j) o[i][j] = fmaf(pp[i][u], v[j], o[i][j]);
       }
     }
+  }
+  if (n_act > 1) {
+    // unnormalised partial (O, m, l) of each row, m in the base-2 score units of this
+    // kernel, at slot (unit, split, row in block) for kv_attn_combine_kernel<..., true>
+    const int64_t unit = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.n_rb + rb;
+#pragma unroll
+    for (int i = 0; i < RW; ++i) {
+      if (live[i]) {
+        const int64_t slot = (unit * p.n_splits + split) * p.rows_per_wg + w * RW + i;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) p.ws_o[slot * D + lane + 64 * j] = o[i][j];
+        if (lane == 0) p.ws_ml[slot] = make_float2(m[i], l[i]);
+      }
+    }
+    return;
   }
 #pragma unroll
   for (int i = 0; i < RW; ++i) {
@@ -3236,7 +3265,7 @@ __global__ __launch_bounds__(256) void kv_split_prefill_merge_kernel(const AttnP
 
 // Merge the split partials of every (sequence, KV head, row block) with more than
 // one active split. 8 output columns per thread, D / 8 threads per row.
-template <int D, bool F16, bool PAGED>
+template <int D, bool F16, bool PAGED, bool OUT_F32 = false>
 __global__ __launch_bounds__(256) void kv_attn_combine_kernel(const AttnParams p) {
   constexpr int TPR = D / 8;
   constexpr int RPB = 256 / TPR;
@@ -3254,7 +3283,9 @@ __global__ __launch_bounds__(256) void kv_attn_combine_kernel(const AttnParams p
   const int d0 = (threadIdx.x % TPR) * 8;
   const int64_t base = static_cast<int64_t>(unit) * p.n_splits * p.rows_per_wg + rl;
 
-  // online merge: m = running reference max, l / o scaled to it
+  // online merge: m = running reference max, l / o scaled to it; the fp32 kernel's
+  // partials carry m in base-2 score units already (scale applied)
+  const float ms = OUT_F32 ? 1.f : p.scale_log2;
   float m = -INFINITY, l = 0.f;
   float o[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   for (int sp0 = 0; sp0 < si.n_act; sp0 += U) {
@@ -3273,8 +3304,8 @@ __global__ __launch_bounds__(256) void kv_attn_combine_kernel(const AttnParams p
       if (sp0 + u >= si.n_act) break;
       const float mn = fmaxf(m, ml[u].x);
       if (mn == -INFINITY) continue;  // neither side has a visible key yet
-      const float a = m == -INFINITY ? 0.f : fast_exp2((m - mn) * p.scale_log2);
-      const float w = ml[u].x == -INFINITY ? 0.f : fast_exp2((ml[u].x - mn) * p.scale_log2);
+      const float a = m == -INFINITY ? 0.f : fast_exp2((m - mn) * ms);
+      const float w = ml[u].x == -INFINITY ? 0.f : fast_exp2((ml[u].x - mn) * ms);
       l = l * a + w * ml[u].y;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -3287,11 +3318,17 @@ __global__ __launch_bounds__(256) void kv_attn_combine_kernel(const AttnParams p
   const float inv = l > 0.f ? 1.f / l : 0.f;
   const int t = r / p.G;
   const int hh = r - t * p.G;
-  uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh + d0;
-  u32x4 w4;
+  if constexpr (OUT_F32) {
+    float* orow = reinterpret_cast<float*>(p.out) + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh + d0;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) w4[j] = pack2<F16>(o[2 * j] * inv, o[2 * j + 1] * inv);
-  *reinterpret_cast<u32x4*>(orow) = w4;
+    for (int j = 0; j < 8; ++j) orow[j] = o[j] * inv;
+  } else {
+    uint16_t* orow = p.out + b * p.o_sb + t * p.o_ss + (kvh * p.G + hh) * p.o_sh + d0;
+    u32x4 w4;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) w4[j] = pack2<F16>(o[2 * j] * inv, o[2 * j + 1] * inv);
+    *reinterpret_cast<u32x4*>(orow) = w4;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -3550,6 +3587,16 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
     } else {
       if (paged) kv_attn_f32_kernel<1, true><<<grid, dim3(256), 0, s>>>(p);
       else kv_attn_f32_kernel<1, false><<<grid, dim3(256), 0, s>>>(p);
+    }
+    if (ls.second) {  // key splits: fold the partials of each row block
+      const dim3 cgrid = to_dim3(ls.second_grid);
+      if (d->head_dim == 128) {
+        if (paged) kv_attn_combine_kernel<128, false, true, true><<<cgrid, dim3(256), 0, s>>>(p);
+        else kv_attn_combine_kernel<128, false, false, true><<<cgrid, dim3(256), 0, s>>>(p);
+      } else {
+        if (paged) kv_attn_combine_kernel<64, false, true, true><<<cgrid, dim3(256), 0, s>>>(p);
+        else kv_attn_combine_kernel<64, false, false, true><<<cgrid, dim3(256), 0, s>>>(p);
+      }
     }
     FDLLM_RETURN_LAUNCH_STATUS("fdllm_kv_attn_fwd");
   }

@@ -72,9 +72,21 @@ static void check_plan(const fdllm_kv_attn_desc& d, const Plan& pl) {
   const i128 len = max_keys > 1 ? max_keys : 1;
   i128 o = 0, ml = 0;  // exact partial sizes
   switch (pl.kind) {
-    case kPlanF32:
-      CHECK(pl.ws_o_bytes == 0 && pl.ws_ml_bytes == 0, "f32 workspace: %s", describe(d));
+    case kPlanF32: {
+      const i128 chunks = cdiv(len, 64);
+      CHECK(static_cast<i128>(pl.n_rb) * pl.rows_per_wg >= R && pl.rows_per_wg == 4 * FDLLM_F32_ROWS_PER_WAVE,
+            "f32 rows: %s", describe(d));
+      CHECK(pl.chunk % 64 == 0 && pl.chunk >= 64 && pl.n_splits >= 1 && pl.n_splits <= kF32MaxSplits &&
+                static_cast<i128>(pl.n_splits) * pl.chunk >= chunks * 64 &&
+                static_cast<i128>(pl.n_splits - 1) * pl.chunk < chunks * 64,
+            "f32 splits %d x %d: %s", pl.n_splits, pl.chunk, describe(d));
+      if (pl.n_splits > 1) {
+        const i128 units = B * hkv * pl.n_rb;
+        o = units * pl.n_splits * pl.rows_per_wg * D * 4;
+        ml = units * pl.n_splits * pl.rows_per_wg * 8;
+      }
       break;
+    }
     case kPlanBalancedDecode: {
       CHECK(Bm <= kBalancedMaxBatch && d.head_dim == 128 && R <= 64, "balanced shape: %s", describe(d));
       CHECK(d.page_table == nullptr || Bm * d.max_pages <= kBalMaxPages, "balanced pages: %s", describe(d));
@@ -192,7 +204,8 @@ static void check_launches(const fdllm_kv_attn_desc& d, const Plan& pl) {
   const i128 total = static_cast<i128>(g.x) * g.y * g.z;
   switch (pl.kind) {
     case kPlanF32:
-      CHECK(static_cast<i128>(g.x) * 4 * FDLLM_F32_ROWS_PER_WAVE >= pl.R && g.y == hkv && g.z == B,
+      CHECK(static_cast<i128>(g.x) == static_cast<i128>(pl.n_rb) * pl.n_splits && g.y == hkv && g.z == B &&
+                ls.second == (pl.n_splits > 1),
             "f32 grid: %s", describe(d));
       break;
     case kPlanBalancedDecode:

@@ -62,6 +62,44 @@ def test_golden_small_decode_fp32(gpu):
                                atol=1e-5, rtol=1e-5)
 
 
+@pytest.mark.parametrize("kv_split", [64, 192, 320, 0, 4096])
+def test_fp32_key_splits(gpu, kv_split):
+    """fp32 kernel with its keys split over workgroups and the partials folded by the
+    combine kernel: 64-key splits (one chunk each), uneven splits (192, 320 keys of 544),
+    the automatic choice and one split; the fp32 golden within 1e-5, and a paged
+    block-causal call with q_start whose row blocks see different key counts (some of a
+    block's splits hold keys past some of its rows' limits) against the float64 brute
+    force."""
+    print(f"case fp32 kv_split={kv_split}", flush=True)
+    z = np.load(GOLDEN / "kv_decode_small.npz")
+    q, k, v = (torch.from_numpy(z[n]) for n in ("q", "k", "v"))
+    seq = torch.from_numpy(z["seqlens"])
+    out = ops.block_attn(q.to(gpu), k.to(gpu), v.to(gpu), seq.to(gpu), float(z["scale"]), kv_split=kv_split)
+    np.testing.assert_allclose(out.cpu().numpy(), z["out"], atol=1e-5, rtol=1e-5)
+    g = torch.Generator().manual_seed(kv_split + 7)
+    B, S, Hq, Hkv, D, Sq, ps = 3, 640, 8, 2, 128, 40, 32
+    seqlens = torch.tensor([600, 0, 233], dtype=torch.int32)
+    q_start = torch.tensor([560, 0, 150], dtype=torch.int32)
+    q2 = torch.randn(B, Sq, Hq, D, generator=g)
+    k2 = torch.randn(B, S, Hkv, D, generator=g)
+    v2 = torch.randn(B, S, Hkv, D, generator=g)
+    n_pages = S // ps
+    pt = torch.randperm(B * n_pages, generator=g).view(B, n_pages).to(torch.int32)
+    kp = torch.empty(B * n_pages, ps, Hkv, D)
+    vp = torch.empty_like(kp)
+    for b in range(B):
+        for j in range(n_pages):
+            kp[pt[b, j]] = k2[b, j * ps:(j + 1) * ps]
+            vp[pt[b, j]] = v2[b, j * ps:(j + 1) * ps]
+    out2 = ops.block_attn(q2.to(gpu), kp.to(gpu), vp.to(gpu), seqlens.to(gpu), None,
+                          mask_mode=_ffi.MASK_BLOCK_CAUSAL, mask_block=32, q_start=q_start.to(gpu),
+                          page_table=pt.to(gpu), page_size=ps, kv_split=kv_split).cpu().numpy()
+    exp = oa.attention_np(q2, k2, v2, seqlens, None, mask_mode=_ffi.MASK_BLOCK_CAUSAL, mask_block=32,
+                          q_start=q_start)
+    np.testing.assert_allclose(out2, exp, atol=1e-5, rtol=1e-5)
+    assert np.count_nonzero(out2[1]) == 0
+
+
 @pytest.mark.parametrize("mask_mode", [_ffi.MASK_SEQLEN, _ffi.MASK_CAUSAL, _ffi.MASK_BLOCK_CAUSAL])
 @pytest.mark.parametrize("paged", [False, True])
 def test_fp32_masks_paged_and_gqa(gpu, mask_mode, paged):
