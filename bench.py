@@ -731,6 +731,37 @@ def calibrate_copies(torch):
             res[f"read_kv_537MB_{layout}_{slots}_slots"] = {"us": round(us, 2),
                                                             "GBs_read": round(n / (us * 1e-6) / 1e9, 1)}
         del k, v
+    # the gather + RMSNorm call and the gathered copy of the same rows at more rows, where
+    # the call's fixed cost (launch, index load, one row round trip) counts less: rows of
+    # 3584 bf16 drawn from [1, 2 x rows, 3584] hidden states, enough slabs cycled (>= 600
+    # MB) that every call reads its rows from HBM, not from the 256 MB last-level cache
+    from fast_v2_amd import _ffi, ops, workloads
+    for rows in (1024, 4096, 16384):
+        wl = workloads.gather_rmsnorm_rows(seed=0, seq_len=2 * rows, rows=rows)
+        n_slabs = max(4, -(-600_000_000 // wl.hidden.numel() // 2))
+        slabs = [wl.hidden.to("cuda")]
+        slabs += [slabs[0].clone() for _ in range(n_slabs - 1)]
+        idx, w = wl.indices.to("cuda"), wl.weight.to("cuda")
+        H = wl.hidden.shape[2]
+        dst = torch.empty(rows, H, dtype=torch.bfloat16, device="cuda")
+
+        def gstep(i, slabs=slabs, idx=idx, w=w, wl=wl):
+            ops.gather_rmsnorm(slabs[i % len(slabs)], idx, w, wl.eps, _ffi.NORM_WEIGHT_AFTER_CAST, False)
+
+        def cstep(i, slabs=slabs, idx=idx, dst=dst, rows=rows, H=H):
+            rc = probes.fdllm_probe_copy_rows(slabs[i % len(slabs)].data_ptr(), H * 2, 2 * rows, idx.data_ptr(),
+                                              dst.data_ptr(), rows, H * 2, _stream_ptr(torch))
+            if rc != 0:
+                raise RuntimeError(f"fdllm_probe_copy_rows failed ({rc})")
+        nb = workloads.gather_bytes(rows, H, 2)
+        steps = 200 if rows < 16384 else 50
+        ug = _time_graph(torch, gstep, steps, 4)
+        uc = _time_graph(torch, cstep, steps, 4)
+        res[f"gather_rmsnorm_{rows}_rows"] = {"us": round(ug, 2), "GBs": round(nb / (ug * 1e-6) / 1e9, 1),
+                                              "copy_us": round(uc, 2),
+                                              "copy_GBs": round((nb - H * 2 - rows * 8) / (uc * 1e-6) / 1e9, 1),
+                                              "slabs": n_slabs}
+        del slabs, dst
     torch.cuda.empty_cache()
     return res
 
