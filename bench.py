@@ -731,6 +731,44 @@ def calibrate_copies(torch):
             res[f"read_kv_537MB_{layout}_{slots}_slots"] = {"us": round(us, 2),
                                                             "GBs_read": round(n / (us * 1e-6) / 1e9, 1)}
         del k, v
+    # the headline's sub-block decode step at four times the length, where its fixed phases
+    # (partition, first tiles, split merge) count less, beside the plain read of the same
+    # rows: batch 16, prefixes U{8192..16352} step 32 + the 32-token block, 64-token pages
+    # (16 x 256 page-table entries, the staging both the kernel and the probe take), 28 / 4
+    # heads, 8 active queries, head-major pages, 2 layer pools (> 600 MB) cycled
+    from fast_v2_amd import ops as _ops, workloads as _wls
+    wl = _wls.kv_decode_paged(seed=0, batch=16, min_prefix=8192, max_prefix=16352, page_size=64)
+    L = 2
+    kpool = torch.empty((L,) + tuple(wl.k_pool.shape), dtype=torch.bfloat16, device="cuda")
+    kpool = kpool.permute(0, 1, 3, 2, 4).contiguous().permute(0, 1, 3, 2, 4)  # head-major pages
+    vpool = torch.empty_like(kpool)
+    gen = torch.Generator(device="cuda").manual_seed(5)
+    kpool.normal_(generator=gen)
+    vpool.normal_(generator=gen)
+    q64, pt64, sl64 = wl.q.to("cuda"), wl.page_table.to("cuda"), wl.seqlens.to("cuda")
+    out64 = torch.empty_like(q64)
+
+    def dstep(i):
+        _ops.block_attn(q64, kpool[i % L], vpool[i % L], sl64, wl.scale, page_table=pt64, page_size=wl.page_size,
+                        out=out64)
+
+    def rstep(i):
+        k_, v_ = kpool[i % L], vpool[i % L]
+        ks_, vs_ = k_.stride(), v_.stride()
+        rc = probes.fdllm_probe_read_kv(k_.data_ptr(), v_.data_ptr(), ks_[0], ks_[1], ks_[2], vs_[0], vs_[1], vs_[2],
+                                        pt64.data_ptr(), pt64.shape[1], wl.page_size, sl64.data_ptr(), 16,
+                                        k_.shape[-2], 64, sink.data_ptr(), _stream_ptr(torch))
+        if rc != 0:
+            raise RuntimeError(f"fdllm_probe_read_kv failed ({rc})")
+    nb64 = _wls.decode_bytes(wl.seqlens, q64.shape[2], kpool.shape[-2], q64.shape[3], q64.shape[1])
+    ud = _time_graph(torch, dstep, 40, 4)
+    ur = _time_graph(torch, rstep, 40, 4)
+    rb64 = int(wl.seqlens.sum()) * kpool.shape[-2] * 128 * 2 * 2
+    res["decode_bs16_long"] = {"us": round(ud, 2), "bytes": nb64, "GBs": round(nb64 / (ud * 1e-6) / 1e9, 1),
+                          "read_us": round(ur, 2), "read_GBs": round(rb64 / (ur * 1e-6) / 1e9, 1),
+                          "step_vs_read": round(ud / ur, 3)}
+    del kpool, vpool
+    torch.cuda.empty_cache()
     # the gather + RMSNorm call and the gathered copy of the same rows at more rows, where
     # the call's fixed cost (launch, index load, one row round trip) counts less: rows of
     # 3584 bf16 drawn from [1, 2 x rows, 3584] hidden states, enough slabs cycled (>= 600
