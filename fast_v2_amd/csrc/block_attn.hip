@@ -3108,13 +3108,37 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
     for (int i = tid; i < n_halves; i += 512) sPg[i] = pt_row[min((k_lo + 32 * i) >> p.page_shift, p.max_pages - 1)];
     __syncthreads();
   }
-  // The first three tiles, then the query fragments, then one wait for all of them.
-  // The compiler sees that wait (a builtin, unlike the loads' asm): it knows qf has
-  // landed and puts no wait of its own for qf inside the loop, where a vmcnt(0) would
-  // drain the tiles in flight every step.
+  // The first tiles, then the query fragments, then one wait for all of them (or, for
+  // the forms without a cache write, the query rows first, below). The compiler sees
+  // that wait (a builtin, unlike the loads' asm): it knows qf has landed and puts no
+  // wait of its own for qf inside the loop, where a vmcnt(0) would drain the tiles in
+  // flight every step; the query-first form reads qf from LDS, which needs no such wait.
   // source of the keys: the cache only (no new rows, or all of them past k_hi), the new
   // rows only (the plain prefill: qs <= k_lo), or both
   const int src_mode = !FUSED || qs >= k_hi ? 0 : (qs <= k_lo ? 1 : 2);
+  // Without the cache write (and in the ping-pong form), the query rows go first, straight
+  // into the LDS of ring slots 2 and 3 (free until tile 2 is issued, after barrier instance
+  // 0): each wave loads the 32 rows it computes, local row lr at the K region 2 TB + 256 lr
+  // (lr < 128) or the V region VREG + 2 TB + 256 (lr - 128), its 16-byte chunks XOR-swizzled
+  // by lr & 15; then tiles 0 and 1; the wait covers the rows and tile 0 only, so the first
+  // step's math starts while tile 1 is in flight (the first steps then wait for tile 1).
+  const int64_t q_span = (static_cast<int64_t>(p.Sq - 1) * p.q_ss + static_cast<int64_t>(p.Hq - 1) * p.q_sh + D) * 2;
+  const bool early_q = !FUSED && FDLLM_PREFILL_PIPE && q_span <= 0x7fffffff;  // uniform
+  if (early_q) {
+    const i32x4 qsrd = make_srd(p.q + b * p.q_sb, static_cast<int>(q_span));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int lr0 = 32 * wave + 4 * i;  // rows lr0 .. lr0 + 3 of this load
+      const int lr = lr0 + (lane >> 4);
+      const int rq = min(row0 + lr, p.R - 1);  // padding rows load a valid row, never used
+      const int tq = rq / p.G;
+      const int hq = rq - tq * p.G;
+      const int off = (tq * static_cast<int>(p.q_ss) + (kvh * p.G + hq) * static_cast<int>(p.q_sh)) * 2 +
+                      (((lane & 15) ^ (lr & 15)) << 4);
+      const uint32_t dst = ring_lds + (lr0 < 128 ? 2 * TB + lr0 * 256 : VREG + 2 * TB + (lr0 - 128) * 256);
+      lds_dma16<false>(qsrd, off, dst);
+    }
+  }
   // tiles 0, 1 (and 2 for the plain form, which keeps three in flight)
   if (ntiles > 0) {
     if (src_mode == 0) {
@@ -3131,12 +3155,21 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
       if (!FDLLM_PREFILL_PIPE) issue(2, 2, 2);
     }
   }
-  {
+  if (early_q) {
+    if (ntiles > 0) wait_vmcnt<4>();  // the rows and tile 0 (tile 1's 4 loads may be in flight)
+    else wait_vmcnt<0>();
+    lds_barrier();  // orders the LDS reads below after the wait
+    const int lr = 32 * wave + n32;
+    const int rbase = lr < 128 ? 2 * TB + lr * 256 : VREG + 2 * TB + (lr - 128) * 256;
+#pragma unroll
+    for (int ks = 0; ks < 8; ++ks)
+      qf[ks] = *reinterpret_cast<const u32x4*>(ring + rbase + (((2 * ks + h) ^ (lr & 15)) << 4));
+  } else {
     const uint16_t* qrow = p.q + b * p.q_sb + t * p.q_ss + (kvh * p.G + hh) * p.q_sh;
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks) qf[ks] = *reinterpret_cast<const u32x4*>(qrow + 16 * ks + 8 * h);
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15): vector memory only
   }
-  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0) expcnt(7) lgkmcnt(15): vector memory only
   FDLLM_STAMP(2, __builtin_amdgcn_s_memrealtime());  // first tiles and Q landed (this wave)
   if constexpr (FUSED) {
     own_store(0);
@@ -3172,7 +3205,9 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
     bool prev_active = false;
     auto pstep = [&](int j, int slot, const int mode) __attribute__((always_inline)) {
       if (grp == 0) {
-        if (j >= 2) wait_vmcnt<4>();  // this wave's loads of tile j have landed (tile j + 1 in flight)
+        // this wave's loads of tile j have landed (tile j + 1 in flight); the prologue's wait
+        // covered tiles 0 and 1, or tile 0 only with the query rows loaded first
+        if (j >= (early_q ? 1 : 2)) wait_vmcnt<4>();
         lds_barrier();
         issue(j + 2, (slot + 2) & 3, mode);
       }
@@ -3181,7 +3216,8 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
       const bool act = j < ntiles && kb < lim_max;  // wave-uniform
       if (act) qk(slot, s);
       if (grp == 1) {
-        if (j >= 1) wait_vmcnt<4>();  // this wave's loads of tile j + 1 have landed (tile j + 2 in flight)
+        // this wave's loads of tile j + 1 have landed (tile j + 2 in flight)
+        if (j >= (early_q ? 0 : 1)) wait_vmcnt<4>();
         lds_barrier();                // instance j + 1
         issue(j + 3, (slot + 3) & 3, mode);
       }
@@ -3189,7 +3225,7 @@ __global__ __launch_bounds__(512, 2) void kv_prefill_ring_kernel(FDLLM_LEAD_PARA
       prev_active = act;
     };
     auto prun = [&](const int mode) __attribute__((always_inline)) {
-      if (grp == 1) {  // instance 0 (tiles 0 and 1 were waited for above)
+      if (grp == 1) {  // instance 0 (tile 0, and tile 1 unless the query rows went first, waited for above)
         lds_barrier();
         issue(2, 2, mode);
       }
