@@ -9,7 +9,8 @@ static-cache layout vs the paged layout (identical outputs); full 32-token
 blocks (224 rows per KV head); split-KV on/off; causal and block-causal masks;
 block-causal prefill with its KV-cache write; ragged lengths, empty sequences,
 a single visible key; fp16; head_dim 64; NaN in every row no query may see (past
-the lengths, unreferenced pages) leaving every kernel family's output unchanged.
+the lengths, unreferenced pages) leaving every kernel family's output unchanged; query
+rows read through non-contiguous strides.
 """
 from pathlib import Path
 
@@ -589,6 +590,47 @@ def _paginate(k, v, page_size, g):
             kp[pg, :n] = k[b, i * page_size:i * page_size + n]
             vp[pg, :n] = v[b, i * page_size:i * page_size + n]
     return kp, vp, pt
+
+
+@pytest.mark.parametrize("layout", ["fused_qkv_slice", "heads_outer"])
+@pytest.mark.parametrize("case", ["sub_block", "full_block", "prefill"])
+def test_strided_query_rows(gpu, case, layout):
+    """Query rows read through their strides: a slice of a fused q / k / v projection
+    ([B, S, Hq + 8, D] cut to its first Hq heads) or a [B, H, S, D] tensor seen as
+    [B, S, H, D]. The split decode kernel loads them per lane; the split prefill
+    (full-block) and prefill kernels without a cache write load them straight into LDS
+    through a descriptor over the sequence's rows. Against the oracle on the same values,
+    and the general kernel on the same call."""
+    g = torch.Generator().manual_seed(sum(map(ord, case + layout)))
+    if case in ("sub_block", "full_block"):
+        wl = workloads.kv_decode_paged(seed=7, batch=4, active=8 if case == "sub_block" else 32)
+        q0, kc, vc, sl, scale = wl.q, wl.k_pool, wl.v_pool, wl.seqlens, wl.scale
+        args = dict(page_table=wl.page_table.to(gpu), page_size=wl.page_size)
+        exp = oa.attention_np(q0.float(), kc.float(), vc.float(), sl, scale, page_table=wl.page_table,
+                              page_size=wl.page_size)
+    else:  # 300 queries x GQA 7 = 2100 rows per KV head: the prefill kernel, block-causal
+        B, Sq, hq, hkv, lens = 1, 300, 28, 4, [700]
+        q0 = torch.randn(B, Sq, hq, 128, generator=g).to(torch.bfloat16)
+        kc = torch.randn(B, max(lens), hkv, 128, generator=g).to(torch.bfloat16)
+        vc = torch.randn(B, max(lens), hkv, 128, generator=g).to(torch.bfloat16)
+        sl = torch.tensor(lens, dtype=torch.int32)
+        scale = None
+        args = dict(mask_mode=_ffi.MASK_BLOCK_CAUSAL, mask_block=32)
+        exp = oa.attention_np(q0.float(), kc.float(), vc.float(), sl, mask_mode=_ffi.MASK_BLOCK_CAUSAL,
+                              mask_block=32)
+    B, Sq, Hq, D = q0.shape
+    if layout == "fused_qkv_slice":
+        big = torch.randn(B, Sq, Hq + 8, D, generator=g).to(q0.dtype)
+        big[:, :, :Hq] = q0
+        q = big.to(gpu)[:, :, :Hq]
+        assert q.stride(1) == (Hq + 8) * D and q.stride(2) == D
+    else:
+        q = q0.transpose(1, 2).contiguous().to(gpu).transpose(1, 2)
+        assert q.stride(1) == D and q.stride(2) == Sq * D
+    print(f"case strided query {case} {layout}", flush=True)
+    for dk in (True, False):
+        out = ops.block_attn(q, kc.to(gpu), vc.to(gpu), sl.to(gpu), scale, decode_kernel=dk, **args)
+        _check(out, exp)
 
 
 @pytest.mark.parametrize("case", [
