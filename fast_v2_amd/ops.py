@@ -182,6 +182,10 @@ def scatter_rows(values: torch.Tensor, indices: torch.Tensor,
                  cache: torch.Tensor, current: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
     """cache[b, indices[b,t]] = values[b, t] (and current[b, indices[b,t]] when given).
 
+    Indices that repeat within a sequence race, as in the reference kernel: each element
+    of such a row ends with that element of one of the rows aimed at it (which one is
+    unspecified, and may differ between the two destinations).
+
     Returns ``current`` (None when it is not given)."""
     dests = [cache] + ([current] if current is not None else [])
     if values.dim() != 3 or indices.dim() != 2 or any(d.dim() != 3 for d in dests):

@@ -108,7 +108,9 @@ int fdllm_gather_rmsnorm(const void* hidden, int64_t hidden_batch_stride, int64_
  * [batch, seq_len, hidden_size] with the given strides. current may be NULL
  * (one destination: BlockSparseCache.scatter_attn_output / scatter_mlp_output,
  * utils/block_sparse_cache.py:112-132). Out-of-range indices are skipped.
- * Duplicate indices within a row race, as in the reference.
+ * Duplicate indices within a row race, as in the reference: each element of such a
+ * destination row ends with that element of one of the rows aimed at it; which one
+ * is unspecified and may differ between the two destinations.
  *
  * Replaces: scatter_and_return_cuda (fused_gather_norm.cu:79-119).
  * ------------------------------------------------------------------------- */

@@ -335,10 +335,12 @@ def test_silu_mul_errors(gpu):
 
 
 def test_scatter_colliding_indices(gpu):
-    """Indices that repeat within a sequence (a collision): the reference kernel's writers
-    race (fused_gather_norm.cu:79-99), so each destination row must hold exactly one of the
-    value rows aimed at it, the same one in both destinations, and every other row keeps its
-    contents."""
+    """Indices that repeat within a sequence (a collision). The reference kernel's writers
+    race element by element (fused_gather_norm.cu:79-99: each thread stores its element to
+    both destinations), so which writer an element ends with is unspecified, and the two
+    destinations may end with different writers. What holds: every element of a
+    destination row aimed at holds that element of one of the value rows aimed at it, in
+    each destination, and every other row keeps its contents."""
     g = torch.Generator().manual_seed(41)
     B, S, T, H = 2, 16, 12, 256
     vals = torch.randn(B, T, H, generator=g).to(torch.bfloat16)
@@ -354,9 +356,10 @@ def test_scatter_colliding_indices(gpu):
             if not src:
                 assert torch.equal(c_out[b, r], cache[b, r]) and torch.equal(u_out[b, r], cur[b, r])
                 continue
-            hits = [t for t in src if torch.equal(c_out[b, r], vals[b, t])]
-            assert hits, f"row {b},{r} holds none of its {len(src)} writers"
-            assert torch.equal(u_out[b, r], c_out[b, r])
+            cand = vals[b, src]  # [writers, H]
+            for name, got in (("cache", c_out[b, r]), ("current", u_out[b, r])):
+                assert bool((got[None] == cand).any(0).all()), \
+                    f"{name} row {b},{r}: an element matches none of its {len(src)} writers"
 
 
 @pytest.mark.parametrize("H", [8, 64])
