@@ -45,6 +45,12 @@ constexpr int kBalancedMaxBatch = 64;  // one wave lane per sequence in the part
 // of 32 queries over 544 keys (96 row blocks): 3 splits 16.4 us, 5 (this target) 13.8 us,
 // 9 splits 15.5 us, no split 27.4 us.
 constexpr int kF32TargetWG = 512;
+// 1: the fp32 kernel's key splits are merged by the last workgroup of each row block to
+// arrive (one arrival counter per row block), where the counters suffice; 0: by a second
+// kernel.
+#ifndef FDLLM_F32_MERGE_IN_KERNEL
+#define FDLLM_F32_MERGE_IN_KERNEL 1
+#endif
 constexpr int kF32MaxSplits = 16;      // fp32 kernel: key splits per row block at most
 constexpr size_t kCounterBytes = 64 * 1024;  // arrival counters at the head of the workspace
 constexpr uint32_t kMaxGridX = 0x7fffffffu;  // grid limits of a launch
@@ -368,6 +374,12 @@ inline bool plan_fuses_cache_write(const fdllm_kv_attn_desc* d, const Plan& pl) 
          (pl.kind == kPlanPrefill || pl.kind == kPlanSplitPrefill);
 }
 
+// The fp32 plan merges its key splits in the kernel (one counter per row block unit).
+inline bool plan_f32_merge_in_kernel(const Plan& pl, int64_t batch, int64_t hkv) {
+  return FDLLM_F32_MERGE_IN_KERNEL && pl.kind == kPlanF32 && pl.n_splits > 1 &&
+         batch * hkv * pl.n_rb <= static_cast<int64_t>(kCounterBytes / sizeof(int));
+}
+
 struct GridDims {
   uint32_t x, y, z;
 };
@@ -411,7 +423,7 @@ inline int plan_launches(const fdllm_kv_attn_desc* d, const Plan& pl, LaunchSet*
       ls->main_grid = GridDims{static_cast<uint32_t>(static_cast<int64_t>(pl.n_rb) * pl.n_splits),
                                static_cast<uint32_t>(hkv), static_cast<uint32_t>(B)};
       ls->main_block = 256;
-      if (pl.n_splits > 1) {
+      if (pl.n_splits > 1 && !plan_f32_merge_in_kernel(pl, B, hkv)) {
         // combine: one workgroup row per (sequence, KV head, row block)
         const int rpb = 256 / (d->head_dim / 8);
         const int64_t units = static_cast<int64_t>(B) * hkv * pl.n_rb;

@@ -1881,8 +1881,10 @@ __device__ __forceinline__ float halves_sum(float v) {
 // Key splits: a row block's keys are cut into splits of p.chunk keys (a multiple of the
 // 64-key chunk) over x = row block + n_rb * split; a row block whose keys fit one split
 // writes its rows directly, otherwise each split writes unnormalised (O, m, l) partials
-// (m in base-2 score units) that kv_attn_combine_kernel<..., true> folds. On the 12 / 2-head
-// block of 32 queries over 544 keys: 27.4 us unsplit, 13.8 us in 5 splits.
+// (m in base-2 score units), which the row block's last split to arrive folds (MERGE), or
+// kv_attn_combine_kernel<..., true> after the kernel. On the 12 / 2-head block of 32
+// queries over 544 keys: 27.4 us unsplit, 13.8 us in 5 splits with the combine kernel,
+// 12.9 us merged in the kernel.
 // query rows per wave of kv_attn_f32_kernel, unsplit: 1: 27.8 us, 2: 36.2 us, 4: 72.9 us
 // (fewer rows per workgroup, more workgroups in flight; the previous one-wave-per-row form
 // without staging: 85 us). The PV products run over every key of a chunk, unrolled,
@@ -1891,7 +1893,7 @@ __device__ __forceinline__ float halves_sum(float v) {
 // (36.1 us).
 // (FDLLM_F32_ROWS_PER_WAVE, the rows per wave, is set in attn_plan.h: the plan sizes the
 // grid from it.)
-template <int DPL, bool PAGED>
+template <int DPL, bool PAGED, bool MERGE>
 __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
   constexpr int D = 64 * DPL;
   constexpr int KS = D + 4;   // K row stride in LDS (floats)
@@ -2041,18 +2043,90 @@ __global__ __launch_bounds__(256) void kv_attn_f32_kernel(const AttnParams p) {
   }
   if (n_act > 1) {
     // unnormalised partial (O, m, l) of each row, m in the base-2 score units of this
-    // kernel, at slot (unit, split, row in block) for kv_attn_combine_kernel<..., true>
+    // kernel, at slot (unit, split, row in block)
     const int64_t unit = (static_cast<int64_t>(b) * p.Hkv + kvh) * p.n_rb + rb;
+    if constexpr (!MERGE) {  // for kv_attn_combine_kernel<..., true>, which follows
 #pragma unroll
-    for (int i = 0; i < RW; ++i) {
-      if (live[i]) {
-        const int64_t slot = (unit * p.n_splits + split) * p.rows_per_wg + w * RW + i;
+      for (int i = 0; i < RW; ++i) {
+        if (live[i]) {
+          const int64_t slot = (unit * p.n_splits + split) * p.rows_per_wg + w * RW + i;
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) p.ws_o[slot * D + lane + 64 * j] = o[i][j];
-        if (lane == 0) p.ws_ml[slot] = make_float2(m[i], l[i]);
+          for (int j = 0; j < DPL; ++j) p.ws_o[slot * D + lane + 64 * j] = o[i][j];
+          if (lane == 0) p.ws_ml[slot] = make_float2(m[i], l[i]);
+        }
       }
+      return;
+    } else {
+      // The last workgroup of the row block to arrive merges its splits: the partials
+      // are written with device-coherent stores (relaxed agent-scope atomic stores: the
+      // sc1 bit, no fence) and acknowledged before the arrival is counted with one
+      // device-scope atomic; the merging workgroup reads them back the same way.
+      float* const po = p.ws_o;
+      float* const pml = reinterpret_cast<float*>(p.ws_ml);
+#pragma unroll
+      for (int i = 0; i < RW; ++i) {
+        if (live[i]) {
+          const int64_t slot = (unit * p.n_splits + split) * p.rows_per_wg + w * RW + i;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j)
+            __hip_atomic_store(po + slot * D + lane + 64 * j, o[i][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if (lane < 2)
+            __hip_atomic_store(pml + 2 * slot + lane, lane == 0 ? m[i] : l[i], __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores acknowledged
+      __syncthreads();
+      __shared__ int s_last;
+      if (tid == 0)
+        s_last = __hip_atomic_fetch_add(&p.ws_cnt[unit], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == n_act - 1;
+      __syncthreads();
+      if (!s_last) return;
+      // each wave merges its own rows over the splits, eight splits' loads in flight at once
+#pragma unroll
+      for (int i = 0; i < RW; ++i) {
+        if (!live[i]) continue;
+        const int64_t slot0 = unit * p.n_splits * p.rows_per_wg + w * RW + i;  // split s at + s rows_per_wg
+        float mm = -INFINITY, ll = 0.f, oo[DPL];
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) oo[j] = 0.f;
+        for (int s0 = 0; s0 < n_act; s0 += 8) {
+          float sm[8], sl[8], so[8][DPL];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const int64_t slot = slot0 + static_cast<int64_t>(min(s0 + u, n_act - 1)) * p.rows_per_wg;
+            sm[u] = __hip_atomic_load(pml + 2 * slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sl[u] = __hip_atomic_load(pml + 2 * slot + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int j = 0; j < DPL; ++j)
+              so[u][j] = __hip_atomic_load(po + slot * D + lane + 64 * j, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
+          float mg = mm;
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (s0 + u < n_act) mg = fmaxf(mg, sm[u]);
+          if (mg == -INFINITY) continue;  // no visible key yet
+          const float a = mm == -INFINITY ? 0.f : fast_exp2(mm - mg);
+          ll *= a;
+#pragma unroll
+          for (int j = 0; j < DPL; ++j) oo[j] *= a;
+#pragma unroll
+          for (int u = 0; u < 8; ++u) {
+            const float wt = (s0 + u < n_act && sm[u] != -INFINITY) ? fast_exp2(sm[u] - mg) : 0.f;
+            ll += wt * sl[u];
+#pragma unroll
+            for (int j = 0; j < DPL; ++j) oo[j] += wt * so[u][j];
+          }
+          mm = mg;
+        }
+        float* out = reinterpret_cast<float*>(p.out) + b * p.o_sb + tq[i] * p.o_ss + hq[i] * p.o_sh;
+        const float inv = ll > 0.f ? 1.f / ll : 0.f;
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) out[lane + 64 * j] = oo[j] * inv;
+      }
+      if (tid == 0) __hip_atomic_store(&p.ws_cnt[unit], 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);  // next call
+      return;
     }
-    return;
   }
 #pragma unroll
   for (int i = 0; i < RW; ++i) {
@@ -3617,12 +3691,23 @@ int kv_attn_launch(const fdllm_kv_attn_desc* d, const Plan& pl, void* workspace,
     // 4 FDLLM_F32_ROWS_PER_WAVE rows of one (sequence, KV head) per workgroup
     const dim3 grid = to_dim3(ls.main_grid);
     const bool paged = d->page_table != nullptr;
+    const bool merge = plan_f32_merge_in_kernel(pl, d->batch, d->num_kv_heads);
     if (d->head_dim == 128) {
-      if (paged) kv_attn_f32_kernel<2, true><<<grid, dim3(256), 0, s>>>(p);
-      else kv_attn_f32_kernel<2, false><<<grid, dim3(256), 0, s>>>(p);
+      if (merge) {
+        if (paged) kv_attn_f32_kernel<2, true, true><<<grid, dim3(256), 0, s>>>(p);
+        else kv_attn_f32_kernel<2, false, true><<<grid, dim3(256), 0, s>>>(p);
+      } else {
+        if (paged) kv_attn_f32_kernel<2, true, false><<<grid, dim3(256), 0, s>>>(p);
+        else kv_attn_f32_kernel<2, false, false><<<grid, dim3(256), 0, s>>>(p);
+      }
     } else {
-      if (paged) kv_attn_f32_kernel<1, true><<<grid, dim3(256), 0, s>>>(p);
-      else kv_attn_f32_kernel<1, false><<<grid, dim3(256), 0, s>>>(p);
+      if (merge) {
+        if (paged) kv_attn_f32_kernel<1, true, true><<<grid, dim3(256), 0, s>>>(p);
+        else kv_attn_f32_kernel<1, false, true><<<grid, dim3(256), 0, s>>>(p);
+      } else {
+        if (paged) kv_attn_f32_kernel<1, true, false><<<grid, dim3(256), 0, s>>>(p);
+        else kv_attn_f32_kernel<1, false, false><<<grid, dim3(256), 0, s>>>(p);
+      }
     }
     if (ls.second) {  // key splits: fold the partials of each row block
       const dim3 cgrid = to_dim3(ls.second_grid);

@@ -205,8 +205,12 @@ static void check_launches(const fdllm_kv_attn_desc& d, const Plan& pl) {
   switch (pl.kind) {
     case kPlanF32:
       CHECK(static_cast<i128>(g.x) == static_cast<i128>(pl.n_rb) * pl.n_splits && g.y == hkv && g.z == B &&
-                ls.second == (pl.n_splits > 1),
+                ls.second == (pl.n_splits > 1 && !plan_f32_merge_in_kernel(pl, d.batch, d.num_kv_heads)),
             "f32 grid: %s", describe(d));
+      // the in-kernel merge counts arrivals per row block unit in the counter region
+      if (plan_f32_merge_in_kernel(pl, d.batch, d.num_kv_heads))
+        CHECK(B * hkv * pl.n_rb <= static_cast<i128>(kCounterBytes / sizeof(int)) && pl.ws_o_bytes > 0,
+              "f32 merge counters: %s", describe(d));
       break;
     case kPlanBalancedDecode:
       CHECK(g.x == static_cast<uint32_t>(pl.n_splits) && g.y == hkv && g.z == 1, "balanced grid: %s", describe(d));
