@@ -183,7 +183,8 @@ typedef struct fdllm_kv_attn_desc {
   int32_t mask_mode;  /* FDLLM_MASK_* */
   int32_t mask_block; /* block length for FDLLM_MASK_BLOCK_CAUSAL */
   int32_t dtype;      /* FDLLM_DTYPE_BF16 or FDLLM_DTYPE_F16 (q, k, v, out); FDLLM_DTYPE_F32 runs a
-                         general fp32 kernel (no workspace, k_new / v_new not accepted) */
+                         general fp32 kernel (k_new / v_new not accepted; a workspace, as
+                         fdllm_kv_attn_workspace_size reports, when it splits the keys) */
   int32_t kv_split;   /* keys per split-KV work item (multiple of 64), 0 = automatic */
   float softmax_scale;
   int32_t flags;      /* FDLLM_ATTN_* bits, 0 = defaults */
