@@ -63,6 +63,27 @@ def test_noalloc_matches_workspace_entry_point(gpu, active):
         torch.testing.assert_close(got.float().cpu(), torch.from_numpy(exp).float(), atol=1e-2, rtol=1e-2)
 
 
+def test_noalloc_fp32_key_splits(gpu):
+    """fp32 calls: the fp32 kernel with its keys split over workgroups, each row block
+    merged by its last split to arrive through the arrival counters at the head of the
+    scratch (the 12 / 2-head block of 32 queries over 544 keys, five splits), then 300 keys
+    on the same scratch; bit-exact against the workspace entry point, within 1e-5 of the
+    float64 oracle."""
+    wl = workloads.kv_decode_fp32_small(seed=0)
+    g = torch.Generator().manual_seed(22)
+    small = (torch.randn(1, 32, 12, 128, generator=g), torch.randn(1, 300, 2, 128, generator=g),
+             torch.randn(1, 300, 2, 128, generator=g), torch.tensor([300], dtype=torch.int32))
+    for i, (q, k, v, sl) in enumerate([(wl.q, wl.k_cache, wl.v_cache, wl.seqlens), small]):
+        print(f"case noalloc fp32 call {i} keys={int(sl[0])}", flush=True)
+        args = (q.to(gpu), k.to(gpu), v.to(gpu), sl.to(gpu), 128 ** -0.5, None, 0)
+        ref, need = _with_workspace(gpu, *args)
+        assert 0 < need <= _ffi.KV_ATTN_SCRATCH_BYTES
+        got = _no_alloc(gpu, *args)
+        assert torch.equal(got, ref), f"call {i}: noalloc output differs from fdllm_kv_attn_fwd"
+        exp = oa.attention_np(q.float(), k.float(), v.float(), sl, 128 ** -0.5)
+        torch.testing.assert_close(got.cpu(), torch.from_numpy(exp).float(), atol=1e-5, rtol=1e-5)
+
+
 def test_noalloc_rejects_calls_beyond_the_scratch(gpu):
     """A call that needs more workspace than the scratch holds is refused before any
     launch, with FDLLM_ERR_WORKSPACE and a message naming the limit."""
