@@ -230,8 +230,19 @@ __global__ __launch_bounds__(64 * kGatherRows) void gather_rmsnorm_vec_kernel(co
   for (int v = 0; v < VPL; ++v) {
     float f[N];
     Vec16<T>::unpack(x[v], f);
+    if constexpr (CAST && std::is_same<T, bf16_t>::value) {
+      // weight * bf16(x * inv): two elements rounded by one v_cvt_pk_bf16_f32 (round to
+      // nearest even on each, as two single conversions), then widened and weighted
 #pragma unroll
-    for (int i = 0; i < N; ++i) f[i] = apply_norm_ct<T, CAST>(f[i], inv, w[v][i]);
+      for (int i = 0; i < N; i += 2) {
+        const uint32_t r = Elt<T>::pack(f[i] * inv, f[i + 1] * inv);
+        f[i] = w[v][i] * Elt<T>::lo(r);
+        f[i + 1] = w[v][i + 1] * Elt<T>::hi(r);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < N; ++i) f[i] = apply_norm_ct<T, CAST>(f[i], inv, w[v][i]);
+    }
     const u32x4 o = Vec16<T>::pack(f);
     if (v < VPL - 1 || last_in) {
       const int c = lane + kWave * v;
