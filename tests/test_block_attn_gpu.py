@@ -414,6 +414,51 @@ def test_split_decode_page_table_staging(gpu, batch, page_size):
                                 page_table=wl.page_table, page_size=page_size))
 
 
+def test_fp32_split_counters_rearm_under_graph_replay(gpu):
+    """The fp32 kernel's key splits are merged by each row block's last split to arrive,
+    which resets the row block's arrival counter: after the call every counter reads zero,
+    and a captured call replayed several times (eager fp32 calls of another shape in
+    between, on the same workspace) matches the eager result on every replay."""
+    wl = workloads.kv_decode_fp32_small(seed=0)
+    q, k, v, sl = wl.q.to(gpu), wl.k_cache.to(gpu), wl.v_cache.to(gpu), wl.seqlens.to(gpu)
+    g = torch.Generator().manual_seed(23)
+    oq = torch.randn(2, 16, 8, 64, generator=g).to(gpu)
+    ok = torch.randn(2, 400, 2, 64, generator=g).to(gpu)
+    ov = torch.randn(2, 400, 2, 64, generator=g).to(gpu)
+    osl = torch.tensor([400, 250], dtype=torch.int32).to(gpu)
+
+    def call():
+        return ops.block_attn(q, k, v, sl, wl.scale)
+
+    def other_call():
+        return ops.block_attn(oq, ok, ov, osl, None, mask_mode=_ffi.MASK_CAUSAL)
+
+    eager = call()
+    _check(eager, oa.attention_np(wl.q.float(), wl.k_cache.float(), wl.v_cache.float(), wl.seqlens, wl.scale),
+           atol=1e-5, rtol=1e-5)
+    other_eager = other_call()
+    _check(other_eager, oa.attention_np(oq.cpu(), ok.cpu(), ov.cpu(), osl.cpu(), mask_mode=_ffi.MASK_CAUSAL),
+           atol=1e-5, rtol=1e-5)
+    torch.cuda.synchronize(gpu)
+    ws = ops._WORKSPACE.get(0, gpu)
+    assert int(ws[:64 * 1024].view(torch.int32).abs().sum()) == 0, "arrival counters not reset"
+    s = torch.cuda.Stream(gpu)
+    s.wait_stream(torch.cuda.current_stream(gpu))
+    with torch.cuda.stream(s):
+        call()  # workspace for this stream exists before capture
+        torch.cuda.synchronize(gpu)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=s):
+            out = call()
+    torch.cuda.current_stream(gpu).wait_stream(s)
+    for _ in range(4):
+        graph.replay()
+        torch.cuda.synchronize(gpu)
+        assert torch.equal(out, eager)
+        assert torch.equal(other_call(), other_eager)
+        torch.cuda.synchronize(gpu)
+
+
 def test_split_decode_counters_rearm_under_graph_replay(gpu):
     """The split decode kernel's last workgroup per KV head merges the partials and
     resets that head's arrival counter: after every call the counters read zero, and a
